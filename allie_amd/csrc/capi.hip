@@ -1,0 +1,707 @@
+// C ABI and host runtime of the engine: model object and weight arena,
+// workspace layout, and the prefill orchestration.  Declarations and the
+// reference interfaces each entry point replaces are in include/allie_amd.h.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/allie_amd.h"
+#include "kernels.hpp"
+
+using namespace allie;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                  \
+  do {                                                                                 \
+    hipError_t _e = (expr);                                                            \
+    if (_e != hipSuccess) return fail(ALLIE_ERR_HIP, "%s: %s", #expr, hipGetErrorString(_e)); \
+  } while (0)
+
+inline size_t align_up(size_t x, size_t a = 256) { return (x + a - 1) / a * a; }
+
+struct LayerW {
+  float *ln1_g, *ln1_b, *b_qkv, *b_o, *ln2_g, *ln2_b, *b_fc, *b_pr;
+  void *w_qkv, *w_o, *w_fc, *w_pr;
+  float *s_qkv, *s_o, *s_fc, *s_pr;  // fp8 scales
+};
+
+constexpr int N_KINDS = 32;
+
+// Kernel probe: HIP events around every launch of one kernel kind inside the
+// forward, for the benchmark's roofline figure (process-wide, not re-entrant).
+struct Probe {
+  int kind = -1;
+  int n = 0;
+  std::vector<hipEvent_t> start, stop;
+} g_probe;
+
+hipError_t probe_mark(int kind, bool before, hipStream_t st) {
+  if (g_probe.kind != kind) return hipSuccess;
+  if (before) {
+    if (g_probe.n >= (int)g_probe.start.size()) return hipSuccess;
+    return hipEventRecord(g_probe.start[g_probe.n], st);
+  }
+  if (g_probe.n >= (int)g_probe.stop.size()) return hipSuccess;
+  return hipEventRecord(g_probe.stop[g_probe.n++], st);
+}
+
+}  // namespace
+
+struct allie_model {
+  allie_config cfg;
+  int d, H, hd, L, V, NH;  // NH: rows of the heads matrix (vocab + 2, padded)
+  int wsz;                 // bytes per block-GEMM weight element
+  int hsz;                 // bytes per heads-matrix element
+  int act_bf16;
+  char* arena = nullptr;
+  size_t arena_bytes = 0;
+  float *wte, *wpe, *ctrl, *lnf_g, *lnf_b, *b_head;
+  void* w_head;
+  std::vector<LayerW> layers;
+  std::vector<uint8_t> set;  // [(L + 1) * N_KINDS]
+  bool ready = false;
+};
+
+namespace {
+
+// Carves the weight arena (base may be null to size it).
+size_t layout_weights(allie_model* m, char* base) {
+  size_t off = 0;
+  auto take = [&](size_t bytes) -> char* {
+    char* p = base ? base + off : nullptr;
+    off += align_up(bytes);
+    return p;
+  };
+  const size_t d = m->d, V = m->V;
+  m->wte = (float*)take(V * d * 4);
+  m->wpe = (float*)take((size_t)m->cfg.n_positions * d * 4);
+  m->ctrl = (float*)take(2 * d * 4);
+  m->lnf_g = (float*)take(d * 4);
+  m->lnf_b = (float*)take(d * 4);
+  m->w_head = take((size_t)m->NH * d * m->hsz);
+  m->b_head = (float*)take((size_t)m->NH * 4);
+  m->layers.resize(m->L);
+  const bool fp8 = m->cfg.mode == ALLIE_MODE_FP8W;
+  for (auto& l : m->layers) {
+    l.ln1_g = (float*)take(d * 4);
+    l.ln1_b = (float*)take(d * 4);
+    l.ln2_g = (float*)take(d * 4);
+    l.ln2_b = (float*)take(d * 4);
+    l.w_qkv = take(3 * d * d * m->wsz);
+    l.b_qkv = (float*)take(3 * d * 4);
+    l.w_o = take(d * d * m->wsz);
+    l.b_o = (float*)take(d * 4);
+    l.w_fc = take(4 * d * d * m->wsz);
+    l.b_fc = (float*)take(4 * d * 4);
+    l.w_pr = take(4 * d * d * m->wsz);
+    l.b_pr = (float*)take(d * 4);
+    l.s_qkv = fp8 ? (float*)take(3 * d * 4) : nullptr;
+    l.s_o = fp8 ? (float*)take(d * 4) : nullptr;
+    l.s_fc = fp8 ? (float*)take(4 * d * 4) : nullptr;
+    l.s_pr = fp8 ? (float*)take(d * 4) : nullptr;
+  }
+  return off;
+}
+
+int check_ready(const allie_model* m) {
+  if (!m) return fail(ALLIE_ERR_ARG, "model is NULL");
+  if (!m->ready) return fail(ALLIE_ERR_STATE, "model not finalised (allie_model_finalize)");
+  return ALLIE_OK;
+}
+
+bool is_layer_kind(int kind) { return kind >= ALLIE_W_LN1_G && kind <= ALLIE_W_PR_B; }
+
+// Workspace of a prefill of B games / T tokens.
+struct PrefillWS {
+  int32_t *lens, *cu, *ids, *pos, *seq_of, *last, *blk_off, *tiles, *status, *slot;
+  int64_t* in_off;
+  float* h;
+  void *x, *qkv, *attn, *ff, *hx;
+  float* z;
+  size_t total;
+};
+
+PrefillWS layout_prefill(const allie_model* m, int B, int T, char* base) {
+  PrefillWS w{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) -> char* {
+    char* p = base ? base + off : nullptr;
+    off += align_up(bytes);
+    return p;
+  };
+  const size_t d = m->d, a = m->act_bf16 ? 2 : 4;
+  const int max_tiles = (m->cfg.max_length + ATTN_Q_TILE - 1) / ATTN_Q_TILE;
+  w.lens = (int32_t*)take((size_t)B * 4);
+  w.cu = (int32_t*)take((size_t)(B + 1) * 4);
+  w.in_off = (int64_t*)take((size_t)B * 8);
+  w.ids = (int32_t*)take((size_t)T * 4);
+  w.pos = (int32_t*)take((size_t)T * 4);
+  w.seq_of = (int32_t*)take((size_t)T * 4);
+  w.slot = (int32_t*)take((size_t)T * 4);
+  w.last = (int32_t*)take((size_t)B * 4);
+  w.blk_off = (int32_t*)take((size_t)(B + 1) * 4);
+  w.tiles = (int32_t*)take((size_t)B * max_tiles * 4);
+  w.status = (int32_t*)take(4);
+  w.h = (float*)take((size_t)T * d * 4);
+  w.x = take((size_t)T * d * a);
+  w.qkv = take((size_t)T * 3 * d * a);
+  w.attn = take((size_t)T * d * a);
+  w.ff = take((size_t)T * 4 * d * a);
+  w.hx = take((size_t)B * d * a);
+  w.z = (float*)take((size_t)B * m->NH * 4);
+  w.total = off;
+  return w;
+}
+
+int gemm(const allie_model* m, const void* A, const void* W, const float* bias, const float* scale,
+         void* C, float* R, int M, int N, int K, int epi, int probe_kind, hipStream_t st) {
+  GemmArgs g{};
+  g.A = A;
+  g.W = W;
+  g.bias = bias;
+  g.scale = scale;
+  g.C = C;
+  g.R = R;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.lda = K;
+  g.ldc = N;
+  g.ldr = N;
+  g.epi = epi;
+  g.wtype = m->cfg.mode == ALLIE_MODE_FP32 ? W_F32 : (m->cfg.mode == ALLIE_MODE_FP8W ? W_FP8 : W_BF16);
+  g.out_f32 = m->cfg.mode == ALLIE_MODE_FP32;
+  HIP_TRY(probe_mark(probe_kind, true, st));
+  hipError_t e = launch_gemm(g, st);
+  if (e != hipSuccess) return fail(ALLIE_ERR_HIP, "gemm M=%d N=%d K=%d: %s", M, N, K, hipGetErrorString(e));
+  HIP_TRY(probe_mark(probe_kind, false, st));
+  return ALLIE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* allie_last_error(void) { return g_err.c_str(); }
+int allie_abi_version(void) { return 1; }
+
+int allie_model_create(const allie_config* cfg, allie_model** out) {
+  if (!cfg || !out) return fail(ALLIE_ERR_ARG, "NULL argument");
+  *out = nullptr;
+  if (cfg->n_layer <= 0 || cfg->d_model <= 0 || cfg->n_head <= 0 || cfg->vocab_size <= 2)
+    return fail(ALLIE_ERR_ARG, "bad config");
+  if (cfg->d_model % cfg->n_head != 0 || cfg->d_model / cfg->n_head != 64)
+    return fail(ALLIE_ERR_ARG, "head_dim must be 64 (d_model %d, n_head %d)", cfg->d_model, cfg->n_head);
+  if (cfg->d_model % 256 != 0 || cfg->d_model > 2048)
+    return fail(ALLIE_ERR_ARG, "d_model must be a multiple of 256 and <= 2048");
+  if (cfg->max_length <= 0 || cfg->max_length > 512 || cfg->max_length > cfg->n_positions)
+    return fail(ALLIE_ERR_ARG, "max_length must be in [1, min(512, n_positions)]");
+  if (cfg->mode < ALLIE_MODE_FP32 || cfg->mode > ALLIE_MODE_FP8W) return fail(ALLIE_ERR_ARG, "bad mode");
+  allie_model* m = new allie_model();
+  m->cfg = *cfg;
+  m->d = cfg->d_model;
+  m->H = cfg->n_head;
+  m->hd = 64;
+  m->L = cfg->n_layer;
+  m->V = cfg->vocab_size;
+  m->NH = (m->V + 2 + 255) / 256 * 256;
+  m->wsz = cfg->mode == ALLIE_MODE_FP32 ? 4 : (cfg->mode == ALLIE_MODE_FP8W ? 1 : 2);
+  m->hsz = cfg->mode == ALLIE_MODE_FP32 ? 4 : 2;
+  m->act_bf16 = cfg->mode != ALLIE_MODE_FP32;
+  m->arena_bytes = layout_weights(m, nullptr);
+  hipError_t e = hipMalloc((void**)&m->arena, m->arena_bytes);
+  if (e != hipSuccess) {
+    const size_t m_bytes = m->arena_bytes;
+    delete m;
+    return fail(ALLIE_ERR_NOMEM, "hipMalloc(%zu): %s", m_bytes, hipGetErrorString(e));
+  }
+  layout_weights(m, m->arena);
+  // zero padding rows of the heads matrix and unset biases
+  e = hipMemset(m->arena, 0, m->arena_bytes);
+  if (e != hipSuccess) {
+    hipFree(m->arena);
+    delete m;
+    return fail(ALLIE_ERR_HIP, "hipMemset: %s", hipGetErrorString(e));
+  }
+  m->set.assign((size_t)(m->L + 1) * N_KINDS, 0);
+  *out = m;
+  return ALLIE_OK;
+}
+
+void allie_model_destroy(allie_model* m) {
+  if (!m) return;
+  if (m->arena) hipFree(m->arena);
+  delete m;
+}
+
+int allie_model_set_weight(allie_model* m, int kind, int layer, const float* src, int64_t rows,
+                           int64_t cols, void* stream) {
+  if (!m || !src) return fail(ALLIE_ERR_ARG, "NULL argument");
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t d = m->d, V = m->V;
+  const int rb = m->act_bf16;  // bf16 modes round biases to bf16 (autocast addmm)
+  const int hb = m->hsz == 2;
+  auto want = [&](int64_t r, int64_t c) -> bool { return rows == r && cols == c; };
+  auto bad_shape = [&]() {
+    return fail(ALLIE_ERR_ARG, "weight kind %d: unexpected shape %lld x %lld", kind, (long long)rows,
+                (long long)cols);
+  };
+  if (is_layer_kind(kind)) {
+    if (layer < 0 || layer >= m->L) return fail(ALLIE_ERR_ARG, "layer %d out of range", layer);
+    LayerW& l = m->layers[layer];
+    const bool fp8 = m->cfg.mode == ALLIE_MODE_FP8W;
+    switch (kind) {
+      case ALLIE_W_LN1_G: case ALLIE_W_LN1_B: case ALLIE_W_LN2_G: case ALLIE_W_LN2_B: {
+        if (rows * cols != d) return bad_shape();
+        float* dst = kind == ALLIE_W_LN1_G ? l.ln1_g : kind == ALLIE_W_LN1_B ? l.ln1_b
+                   : kind == ALLIE_W_LN2_G ? l.ln2_g : l.ln2_b;
+        HIP_TRY(hipMemcpyAsync(dst, src, d * 4, hipMemcpyDeviceToDevice, st));
+        break;
+      }
+      case ALLIE_W_QKV_B: case ALLIE_W_O_B: case ALLIE_W_FC_B: case ALLIE_W_PR_B: {
+        const int64_t n = kind == ALLIE_W_QKV_B ? 3 * d : kind == ALLIE_W_FC_B ? 4 * d : d;
+        if (rows * cols != n) return bad_shape();
+        float* dst = kind == ALLIE_W_QKV_B ? l.b_qkv : kind == ALLIE_W_O_B ? l.b_o
+                   : kind == ALLIE_W_FC_B ? l.b_fc : l.b_pr;
+        HIP_TRY(launch_convert(src, n, dst, 0, rb, st));
+        break;
+      }
+      case ALLIE_W_QKV_W: case ALLIE_W_O_W: case ALLIE_W_FC_W: case ALLIE_W_PR_W: {
+        if (fp8) return fail(ALLIE_ERR_ARG, "fp8 mode: set block GEMM weights with allie_model_set_weight_fp8");
+        int64_t in = d, outf = d;
+        void* dst = l.w_o;
+        if (kind == ALLIE_W_QKV_W) { outf = 3 * d; dst = l.w_qkv; }
+        if (kind == ALLIE_W_FC_W) { outf = 4 * d; dst = l.w_fc; }
+        if (kind == ALLIE_W_PR_W) { in = 4 * d; dst = l.w_pr; }
+        if (!want(in, outf)) return bad_shape();
+        HIP_TRY(launch_transpose_convert(src, (int)in, (int)outf, dst, rb, (int)in, st));
+        break;
+      }
+      default: return fail(ALLIE_ERR_ARG, "unknown weight kind %d", kind);
+    }
+    m->set[(size_t)(layer + 1) * N_KINDS + (kind - ALLIE_W_LN1_G)] = 1;
+    return ALLIE_OK;
+  }
+  switch (kind) {
+    case ALLIE_W_WTE:
+      if (!want(V, d)) return bad_shape();
+      HIP_TRY(hipMemcpyAsync(m->wte, src, V * d * 4, hipMemcpyDeviceToDevice, st));
+      HIP_TRY(launch_convert(src, V * d, m->w_head, hb, 0, st));
+      break;
+    case ALLIE_W_WPE:
+      if (!want(m->cfg.n_positions, d)) return bad_shape();
+      HIP_TRY(hipMemcpyAsync(m->wpe, src, (size_t)m->cfg.n_positions * d * 4, hipMemcpyDeviceToDevice, st));
+      break;
+    case ALLIE_W_CTRL:
+      if (!want(2, d)) return bad_shape();
+      HIP_TRY(hipMemcpyAsync(m->ctrl, src, 2 * d * 4, hipMemcpyDeviceToDevice, st));
+      break;
+    case ALLIE_W_LNF_G: case ALLIE_W_LNF_B:
+      if (rows * cols != d) return bad_shape();
+      HIP_TRY(hipMemcpyAsync(kind == ALLIE_W_LNF_G ? m->lnf_g : m->lnf_b, src, d * 4,
+                             hipMemcpyDeviceToDevice, st));
+      break;
+    case ALLIE_W_VALUE_W: case ALLIE_W_TIME_W: {
+      if (rows * cols != d) return bad_shape();
+      const int64_t row = kind == ALLIE_W_VALUE_W ? V : V + 1;
+      char* dst = (char*)m->w_head + row * d * m->hsz;
+      HIP_TRY(launch_convert(src, d, dst, hb, 0, st));
+      break;
+    }
+    case ALLIE_W_VALUE_B: case ALLIE_W_TIME_B: {
+      if (rows * cols != 1) return bad_shape();
+      const int64_t row = kind == ALLIE_W_VALUE_B ? V : V + 1;
+      HIP_TRY(launch_convert(src, 1, m->b_head + row, 0, rb, st));
+      break;
+    }
+    default: return fail(ALLIE_ERR_ARG, "unknown weight kind %d", kind);
+  }
+  m->set[kind] = 1;
+  return ALLIE_OK;
+}
+
+int allie_model_set_weight_fp8(allie_model* m, int kind, int layer, const uint8_t* q,
+                               const float* scale, int64_t out_features, int64_t in_features,
+                               void* stream) {
+  if (!m || !q || !scale) return fail(ALLIE_ERR_ARG, "NULL argument");
+  if (m->cfg.mode != ALLIE_MODE_FP8W) return fail(ALLIE_ERR_ARG, "model is not in fp8 mode");
+  if (layer < 0 || layer >= m->L) return fail(ALLIE_ERR_ARG, "layer %d out of range", layer);
+  hipStream_t st = (hipStream_t)stream;
+  LayerW& l = m->layers[layer];
+  const int64_t d = m->d;
+  void* dst;
+  float* sdst;
+  int64_t in = d, outf = d;
+  switch (kind) {
+    case ALLIE_W_QKV_W: dst = l.w_qkv; sdst = l.s_qkv; outf = 3 * d; break;
+    case ALLIE_W_O_W: dst = l.w_o; sdst = l.s_o; break;
+    case ALLIE_W_FC_W: dst = l.w_fc; sdst = l.s_fc; outf = 4 * d; break;
+    case ALLIE_W_PR_W: dst = l.w_pr; sdst = l.s_pr; in = 4 * d; break;
+    default: return fail(ALLIE_ERR_ARG, "fp8 weights are only for the block GEMMs (kind %d)", kind);
+  }
+  if (out_features != outf || in_features != in)
+    return fail(ALLIE_ERR_ARG, "fp8 weight kind %d: unexpected shape %lld x %lld", kind,
+                (long long)out_features, (long long)in_features);
+  HIP_TRY(hipMemcpyAsync(dst, q, outf * in, hipMemcpyDeviceToDevice, st));
+  HIP_TRY(hipMemcpyAsync(sdst, scale, outf * 4, hipMemcpyDeviceToDevice, st));
+  m->set[(size_t)(layer + 1) * N_KINDS + (kind - ALLIE_W_LN1_G)] = 1;
+  return ALLIE_OK;
+}
+
+int allie_model_finalize(allie_model* m) {
+  if (!m) return fail(ALLIE_ERR_ARG, "model is NULL");
+  for (int k = ALLIE_W_WTE; k <= ALLIE_W_TIME_B; ++k)
+    if (!m->set[k]) return fail(ALLIE_ERR_STATE, "global weight kind %d not set", k);
+  for (int l = 0; l < m->L; ++l)
+    for (int k = ALLIE_W_LN1_G; k <= ALLIE_W_PR_B; ++k)
+      if (!m->set[(size_t)(l + 1) * N_KINDS + (k - ALLIE_W_LN1_G)])
+        return fail(ALLIE_ERR_STATE, "layer %d weight kind %d not set", l, k);
+  m->ready = true;
+  return ALLIE_OK;
+}
+
+int allie_pack_ragged(const uint32_t* words, const int32_t* lens, int n_seq, int max_len,
+                      int block, int first_block, int max_blocks, int capacity,
+                      int32_t* cu_seqlens, int64_t* in_off, int32_t* ids, int32_t* pos,
+                      int32_t* seq_of, int32_t* last_idx, int32_t* blk_off,
+                      int32_t* block_table, int32_t* slot, int32_t* status, void* stream) {
+  if (n_seq < 0 || max_len <= 0 || block <= 0 || max_blocks < 0 || capacity < 0)
+    return fail(ALLIE_ERR_ARG, "bad pack sizes");
+  if (!lens || !cu_seqlens || !in_off || !last_idx || !blk_off || !status ||
+      (capacity > 0 && (!ids || !pos || !seq_of) ) || (n_seq > 0 && !words))
+    return fail(ALLIE_ERR_ARG, "NULL argument");
+  PackArgs p{};
+  p.words = words;
+  p.lens = lens;
+  p.B = n_seq;
+  p.max_len = max_len;
+  p.block = block;
+  p.first_block = first_block;
+  p.max_blocks = max_blocks;
+  p.q_tile = ATTN_Q_TILE;
+  p.capacity = capacity;
+  p.cu_seqlens = cu_seqlens;
+  p.in_off = in_off;
+  p.ids = ids;
+  p.pos = pos;
+  p.seq_of = seq_of;
+  p.last_idx = last_idx;
+  p.blk_off = blk_off;
+  p.block_table = block_table;
+  p.slot = slot;
+  p.tiles = nullptr;
+  p.status = status;
+  HIP_TRY(launch_pack(p, (hipStream_t)stream));
+  return ALLIE_OK;
+}
+
+size_t allie_prefill_workspace_bytes(const allie_model* m, int n_seq, int n_tokens) {
+  if (!m || n_seq < 0 || n_tokens < 0) return 0;
+  return layout_prefill(m, n_seq, n_tokens, nullptr).total;
+}
+
+size_t allie_kv_block_bytes(const allie_model* m) {
+  if (!m) return 0;
+  return (size_t)m->L * 2 * m->H * KV_BLOCK * m->hd * (m->act_bf16 ? 2 : 4);
+}
+
+int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_host, int n_seq,
+                  float temperature, const uint32_t* legal, int legal_words,
+                  const allie_outputs* out, void* kv_pool, int kv_pool_blocks, int first_block,
+                  void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_ready(m);
+  if (rc) return rc;
+  if (n_seq <= 0 || !words || !lens_host || !out || !workspace)
+    return fail(ALLIE_ERR_ARG, "bad prefill arguments");
+  if (!out->value || !out->time || !out->top1 || !out->max_logit || !out->lse)
+    return fail(ALLIE_ERR_ARG, "value/time/top1/max_logit/lse outputs are required");
+  if (legal && legal_words * 32 < 1968) return fail(ALLIE_ERR_ARG, "legal mask too narrow");
+  const int max_len = m->cfg.max_length;
+  int64_t T = 0, n_tiles = 0, n_blocks = 0;
+  for (int i = 0; i < n_seq; ++i) {
+    if (lens_host[i] <= 0) return fail(ALLIE_ERR_LENGTH, "game %d is empty", i);
+    const int n = lens_host[i] < max_len ? lens_host[i] : max_len;
+    T += n;
+    n_tiles += (n + ATTN_Q_TILE - 1) / ATTN_Q_TILE;
+    n_blocks += (n + KV_BLOCK - 1) / KV_BLOCK;
+  }
+  if (T > (int64_t)1 << 30) return fail(ALLIE_ERR_ARG, "too many tokens");
+  if (kv_pool && (first_block < 0 || first_block + n_blocks > kv_pool_blocks))
+    return fail(ALLIE_ERR_LENGTH, "KV pool too small: need blocks [%d, %lld), have %d", first_block,
+                (long long)(first_block + n_blocks), kv_pool_blocks);
+  PrefillWS w = layout_prefill(m, n_seq, (int)T, (char*)workspace);
+  if (workspace_bytes < w.total)
+    return fail(ALLIE_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, w.total);
+  hipStream_t st = (hipStream_t)stream;
+  const int d = m->d, L = m->L, act = m->act_bf16;
+  const float eps = m->cfg.eps;
+
+  HIP_TRY(hipMemcpyAsync(w.lens, lens_host, (size_t)n_seq * 4, hipMemcpyHostToDevice, st));
+  PackArgs p{};
+  p.words = words;
+  p.lens = w.lens;
+  p.B = n_seq;
+  p.max_len = max_len;
+  p.block = KV_BLOCK;
+  p.first_block = first_block;
+  p.max_blocks = (max_len + KV_BLOCK - 1) / KV_BLOCK;
+  p.q_tile = ATTN_Q_TILE;
+  p.capacity = (int)T;
+  p.cu_seqlens = w.cu;
+  p.in_off = w.in_off;
+  p.ids = w.ids;
+  p.pos = w.pos;
+  p.seq_of = w.seq_of;
+  p.last_idx = w.last;
+  p.blk_off = w.blk_off;
+  p.block_table = nullptr;
+  p.slot = kv_pool ? w.slot : nullptr;
+  p.tiles = w.tiles;
+  p.status = w.status;
+  HIP_TRY(launch_pack(p, st));
+
+  EmbedArgs ea{};
+  ea.ids = w.ids;
+  ea.pos = w.pos;
+  ea.T = (int)T;
+  ea.d = d;
+  ea.vocab = m->V;
+  ea.wte = m->wte;
+  ea.wpe = m->wpe;
+  ea.ctrl = m->ctrl;
+  ea.ln_g = m->layers[0].ln1_g;
+  ea.ln_b = m->layers[0].ln1_b;
+  ea.eps = eps;
+  ea.h = w.h;
+  ea.x = w.x;
+  ea.act_bf16 = act;
+  HIP_TRY(launch_embed_ln(ea, st));
+
+  AttnVarlenArgs aa{};
+  aa.qkv = w.qkv;
+  aa.cu_seqlens = w.cu;
+  aa.tiles = w.tiles;
+  aa.n_tiles = (int)n_tiles;
+  aa.B = n_seq;
+  aa.T = (int)T;
+  aa.n_head = m->H;
+  aa.head_dim = m->hd;
+  aa.scale = 0.125f;  // 1 / sqrt(64)
+  aa.out = w.attn;
+  aa.act_bf16 = act;
+
+  LNArgs ln{};
+  ln.h = w.h;
+  ln.rows = ln.rows_out = (int)T;
+  ln.d = d;
+  ln.eps = eps;
+  ln.y = w.x;
+  ln.act_bf16 = act;
+
+  const int Ti = (int)T;
+  for (int li = 0; li < L; ++li) {
+    const LayerW& l = m->layers[li];
+    if ((rc = gemm(m, w.x, l.w_qkv, l.b_qkv, l.s_qkv, w.qkv, nullptr, Ti, 3 * d, d, EPI_STORE, ALLIE_PROBE_QKV, st))) return rc;
+    if (kv_pool) {
+      KVWriteArgs kw{};
+      kw.qkv = w.qkv;
+      kw.slot = w.slot;
+      kw.T = Ti;
+      kw.n_layer = L;
+      kw.layer = li;
+      kw.n_head = m->H;
+      kw.head_dim = m->hd;
+      kw.pool = kv_pool;
+      kw.act_bf16 = act;
+      HIP_TRY(launch_kv_write(kw, st));
+    }
+    HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, true, st));
+    HIP_TRY(launch_attn_varlen(aa, st));
+    HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, false, st));
+    if ((rc = gemm(m, w.attn, l.w_o, l.b_o, l.s_o, nullptr, w.h, Ti, d, d, EPI_RESID, ALLIE_PROBE_PROJ, st))) return rc;
+    ln.g = l.ln2_g;
+    ln.b = l.ln2_b;
+    HIP_TRY(launch_layernorm(ln, st));
+    if ((rc = gemm(m, w.x, l.w_fc, l.b_fc, l.s_fc, w.ff, nullptr, Ti, 4 * d, d, EPI_GELU, ALLIE_PROBE_FC, st))) return rc;
+    if ((rc = gemm(m, w.ff, l.w_pr, l.b_pr, l.s_pr, nullptr, w.h, Ti, d, 4 * d, EPI_RESID, ALLIE_PROBE_FC2, st))) return rc;
+    if (li + 1 < L) {
+      ln.g = m->layers[li + 1].ln1_g;
+      ln.b = m->layers[li + 1].ln1_b;
+      HIP_TRY(launch_layernorm(ln, st));
+    }
+  }
+  // heads on the last token of every game
+  LNArgs lf{};
+  lf.h = w.h;
+  lf.row_idx = w.last;
+  lf.rows = lf.rows_out = n_seq;
+  lf.d = d;
+  lf.g = m->lnf_g;
+  lf.b = m->lnf_b;
+  lf.eps = eps;
+  lf.y = w.hx;
+  lf.act_bf16 = act;
+  HIP_TRY(launch_layernorm(lf, st));
+  {
+    GemmArgs g{};
+    g.A = w.hx;
+    g.W = m->w_head;
+    g.bias = m->b_head;
+    g.C = w.z;
+    g.M = n_seq;
+    g.N = m->NH;
+    g.K = d;
+    g.lda = d;
+    g.ldc = m->NH;
+    g.epi = EPI_STORE;
+    g.wtype = act ? W_BF16 : W_F32;
+    g.out_f32 = 1;
+    hipError_t e = launch_gemm(g, st);
+    if (e != hipSuccess) return fail(ALLIE_ERR_HIP, "heads gemm: %s", hipGetErrorString(e));
+  }
+  HeadsArgs ha{};
+  ha.z = w.z;
+  ha.B = n_seq;
+  ha.ldz = m->NH;
+  ha.vocab = m->V;
+  ha.n_moves = 1968;
+  ha.value_col = m->V;
+  ha.time_col = m->V + 1;
+  ha.temperature = temperature > 1e-5f ? temperature : 1e-5f;
+  ha.legal = legal;
+  ha.legal_words = legal_words;
+  ha.logits = out->logits;
+  ha.value = out->value;
+  ha.time = out->time;
+  ha.top1 = out->top1;
+  ha.lse = out->lse;
+  ha.max_logit = out->max_logit;
+  ha.emulate_bf16 = act;
+  HIP_TRY(launch_heads(ha, st));
+  return ALLIE_OK;
+}
+
+int allie_probe_begin(int kind, int max_launches) {
+  if (kind < ALLIE_PROBE_QKV || kind > ALLIE_PROBE_ATTN || max_launches <= 0)
+    return fail(ALLIE_ERR_ARG, "bad probe arguments");
+  for (auto e : g_probe.start) hipEventDestroy(e);
+  for (auto e : g_probe.stop) hipEventDestroy(e);
+  g_probe = Probe();
+  g_probe.start.resize(max_launches);
+  g_probe.stop.resize(max_launches);
+  for (int i = 0; i < max_launches; ++i) {
+    HIP_TRY(hipEventCreate(&g_probe.start[i]));
+    HIP_TRY(hipEventCreate(&g_probe.stop[i]));
+  }
+  g_probe.kind = kind;
+  return ALLIE_OK;
+}
+
+int allie_probe_end(float* total_ms_host, int* n_launches_host) {
+  if (!total_ms_host || !n_launches_host) return fail(ALLIE_ERR_ARG, "NULL argument");
+  float tot = 0.f;
+  const int n = g_probe.n;
+  for (int i = 0; i < n; ++i) {
+    HIP_TRY(hipEventSynchronize(g_probe.stop[i]));
+    float ms = 0.f;
+    HIP_TRY(hipEventElapsedTime(&ms, g_probe.start[i], g_probe.stop[i]));
+    tot += ms;
+  }
+  for (auto e : g_probe.start) hipEventDestroy(e);
+  for (auto e : g_probe.stop) hipEventDestroy(e);
+  g_probe = Probe();
+  *total_ms_host = tot;
+  *n_launches_host = n;
+  return ALLIE_OK;
+}
+
+int allie_gemm(const void* A, const void* W, const float* bias, const float* scale, void* C,
+               float* R, int M, int N, int K, int epi, int wtype, int out_f32, void* stream) {
+  if (!A || !W || M < 0 || N <= 0 || K <= 0) return fail(ALLIE_ERR_ARG, "bad gemm arguments");
+  if (epi < EPI_STORE || epi > EPI_RESID || wtype < W_BF16 || wtype > W_FP8)
+    return fail(ALLIE_ERR_ARG, "bad gemm mode");
+  if ((epi == EPI_RESID && !R) || (epi != EPI_RESID && !C) || (wtype == W_FP8 && !scale))
+    return fail(ALLIE_ERR_ARG, "missing gemm output/scale");
+  GemmArgs g{};
+  g.A = A;
+  g.W = W;
+  g.bias = bias;
+  g.scale = scale;
+  g.C = C;
+  g.R = R;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.lda = K;
+  g.ldc = N;
+  g.ldr = N;
+  g.epi = epi;
+  g.wtype = wtype;
+  g.out_f32 = wtype == W_F32 ? 1 : out_f32;
+  if (wtype != W_F32 && !gemm_mfma_supported(g))
+    return fail(ALLIE_ERR_ARG, "MFMA gemm needs N %% 256 == 0 and K %% 64 == 0 (N=%d K=%d)", N, K);
+  if (wtype == W_FP8 && out_f32) return fail(ALLIE_ERR_ARG, "fp8 gemm has bf16 output only");
+  if (wtype != W_F32 && out_f32 && epi != EPI_STORE)
+    return fail(ALLIE_ERR_ARG, "fp32 output only with the store epilogue");
+  HIP_TRY(launch_gemm(g, (hipStream_t)stream));
+  return ALLIE_OK;
+}
+
+int allie_attn_varlen(const void* qkv, const int32_t* cu_seqlens, const int32_t* tiles,
+                      int n_tiles, int n_seq, int n_tokens, int n_head, int head_dim,
+                      float scale, void* out, int act_bf16, void* stream) {
+  if (!qkv || !cu_seqlens || !out || (act_bf16 && !tiles) || head_dim != 64 || n_head <= 0)
+    return fail(ALLIE_ERR_ARG, "bad attention arguments");
+  AttnVarlenArgs a{};
+  a.qkv = qkv;
+  a.cu_seqlens = cu_seqlens;
+  a.tiles = tiles;
+  a.n_tiles = n_tiles;
+  a.B = n_seq;
+  a.T = n_tokens;
+  a.n_head = n_head;
+  a.head_dim = head_dim;
+  a.scale = scale;
+  a.out = out;
+  a.act_bf16 = act_bf16;
+  HIP_TRY(launch_attn_varlen(a, (hipStream_t)stream));
+  return ALLIE_OK;
+}
+
+int allie_layernorm(const float* h, const int32_t* row_idx, int rows, int rows_out, int d,
+                    const float* g, const float* b, float eps, void* y, int act_bf16,
+                    void* stream) {
+  if (!h || !g || !b || !y || rows < 0 || rows_out < rows || d % 256 != 0 || d > 2048)
+    return fail(ALLIE_ERR_ARG, "bad layernorm arguments");
+  LNArgs a{};
+  a.h = h;
+  a.row_idx = row_idx;
+  a.rows = rows;
+  a.rows_out = rows_out;
+  a.d = d;
+  a.g = g;
+  a.b = b;
+  a.eps = eps;
+  a.y = y;
+  a.act_bf16 = act_bf16;
+  HIP_TRY(launch_layernorm(a, (hipStream_t)stream));
+  return ALLIE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,63 @@
+// Shared device helpers for the Allie gfx950 kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define ALLIE_DEV __device__ __forceinline__
+
+typedef uint16_t bf16_t;  // storage type: raw bf16 bits
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
+ALLIE_DEV uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+ALLIE_DEV float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
+ALLIE_DEV float round_bf16(float f) { return bf2f(f2bf(f)); }
+ALLIE_DEV uint32_t pack_bf16x2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
+
+// OCP fp8 e4m3fn -> fp32 (exact).  bias 7, no infinities, 0x7f/0xff = NaN.
+ALLIE_DEV float fp8e4m3_to_f32(uint32_t v) {
+  uint32_t s = (v & 0x80u) << 24;
+  uint32_t e = (v >> 3) & 0xfu;
+  uint32_t m = v & 0x7u;
+  if (e == 0) {  // subnormal: m * 2^-9
+    float f = (float)m * 0.001953125f;
+    return __uint_as_float(__float_as_uint(f) | s);
+  }
+  if (e == 15 && m == 7) return __uint_as_float(0x7fc00000u | s);
+  return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
+}
+// fp8 e4m3fn -> bf16 bits (exact: 3 mantissa bits fit in bf16's 7)
+ALLIE_DEV uint32_t fp8e4m3_to_bf16(uint32_t v) { return __float_as_uint(fp8e4m3_to_f32(v)) >> 16; }
+
+ALLIE_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+ALLIE_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// tanh from exp: tanh(x) = 1 - 2 / (exp(2x) + 1); saturates cleanly for |x| large.
+ALLIE_DEV float tanh_fast(float x) {
+  float e = __expf(2.0f * x);
+  return 1.0f - 2.0f / (e + 1.0f);
+}
+
+// gelu_new (tanh form), evaluated in fp32.
+ALLIE_DEV float gelu_tanh(float x) {
+  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
+  float inner = k0 * (x + 0.044715f * (x * x * x));
+  return (0.5f * x) * (1.0f + tanhf(inner));
+}

@@ -1,0 +1,169 @@
+// Launch interfaces of the Allie gfx950 kernels (host side of each .hip file).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace allie {
+
+// ---------------------------------------------------------------- packing
+struct PackArgs {
+  const uint32_t* words;  // flat tokenizer words, games back to back
+  const int32_t* lens;    // [B] words per game (before truncation)
+  int B, max_len, block, first_block, max_blocks, q_tile;
+  int capacity;           // length of ids/pos/seq_of/slot
+  int32_t* cu_seqlens;    // [B+1]
+  int64_t* in_off;        // [B] word offset of each game (scratch)
+  int32_t* ids;           // [T]
+  int32_t* pos;           // [T]
+  int32_t* seq_of;        // [T]
+  int32_t* last_idx;      // [B]
+  int32_t* blk_off;       // [B+1]
+  int32_t* block_table;   // [B][max_blocks] or null
+  int32_t* slot;          // [T] or null
+  int32_t* tiles;         // attention query tiles or null
+  int32_t* status;        // [1]: bit 1 empty game, 2 capacity exceeded, 4 table too small
+};
+hipError_t launch_pack(const PackArgs& a, hipStream_t st);
+
+// ------------------------------------------------- embedding / LayerNorm
+// act_bf16: activations written as bf16 (else fp32); emulate_bf16: apply the
+// bf16-autocast rounding points of the reference (Elo control matmul).
+struct EmbedArgs {
+  const int32_t* ids;
+  const int32_t* pos;
+  int T, d, vocab;
+  const float* wte;   // [vocab][d]
+  const float* wpe;   // [n_pos][d]
+  const float* ctrl;  // [2][d]
+  const float* ln_g;  // first block's ln_1
+  const float* ln_b;
+  float eps;
+  float* h;           // [T][d] residual stream (fp32)
+  void* x;            // [T][d] LayerNorm output (bf16 or fp32)
+  int act_bf16;
+};
+hipError_t launch_embed_ln(const EmbedArgs& a, hipStream_t st);
+
+struct LNArgs {
+  const float* h;          // [rows][d] fp32
+  const int32_t* row_idx;  // optional gather: output row r reads h[row_idx[r]]
+  int rows, rows_out, d;   // rows_out >= rows: extra rows are zero-filled
+  const float* g;
+  const float* b;
+  float eps;
+  void* y;                 // [rows_out][d] bf16 or fp32
+  int act_bf16;
+};
+hipError_t launch_layernorm(const LNArgs& a, hipStream_t st);
+
+// ------------------------------------------------------------------ GEMM
+// C[m, n] = sum_k A[m, k] * W[n, k]   (both operands K-contiguous)
+enum Epilogue {
+  EPI_STORE = 0,   // y = acc + bias                        -> C
+  EPI_GELU = 1,    // y = gelu(acc + bias)                  -> C
+  EPI_RESID = 2,   // R[m, n] += acc + bias                 (R fp32, in place)
+};
+enum WType { W_BF16 = 0, W_F32 = 1, W_FP8 = 2 };
+
+struct GemmArgs {
+  const void* A;       // [M][lda] bf16 (W_BF16 / W_FP8) or fp32 (W_F32)
+  const void* W;       // [N][K]
+  const float* bias;   // [N] or null
+  const float* scale;  // [N] per-output-channel weight scale (W_FP8) or null
+  void* C;             // [M][ldc] bf16 or fp32
+  float* R;            // [M][ldr] residual (EPI_RESID)
+  int M, N, K, lda, ldc, ldr;
+  int epi;
+  int wtype;
+  int out_f32;         // store C as fp32 (else bf16)
+};
+hipError_t launch_gemm(const GemmArgs& a, hipStream_t st);
+bool gemm_mfma_supported(const GemmArgs& a);
+
+// ------------------------------------------------------------- attention
+// Varlen causal self-attention over packed sequences (no KV cache):
+// qkv [T][3d] (q | k | v column blocks, heads as head_dim column groups),
+// out [T][d].
+struct AttnVarlenArgs {
+  const void* qkv;
+  const int32_t* cu_seqlens;
+  const int32_t* tiles;  // (seq << 5) | q_tile, heaviest first
+  int n_tiles, B, T, n_head, head_dim;
+  float scale;
+  void* out;
+  int act_bf16;
+};
+constexpr int ATTN_Q_TILE = 64;
+hipError_t launch_attn_varlen(const AttnVarlenArgs& a, hipStream_t st);
+
+// Paged attention: queries are new tokens of B sequences; keys/values come
+// from a paged pool (block = 16 tokens) that already holds the new tokens.
+// Pool layout: [block][layer][k|v][head][16][head_dim]; slot = block*16 + offset.
+constexpr int KV_BLOCK = 16;
+struct KVWriteArgs {
+  const void* qkv;       // [T][3d]
+  const int32_t* slot;   // [T]
+  int T, n_layer, layer, n_head, head_dim;
+  void* pool;
+  int act_bf16;
+};
+hipError_t launch_kv_write(const KVWriteArgs& a, hipStream_t st);
+
+struct AttnPagedArgs {
+  const void* qkv;            // [T][3d]: queries of the new tokens
+  const int32_t* q_seq;       // [T] sequence of each query
+  const int32_t* q_pos;       // [T] position of each query (keys 0..pos visible)
+  const int32_t* block_table; // [B][max_blocks]
+  int max_blocks, T, n_head, head_dim;
+  const void* pool;           // layer base
+  float scale;
+  void* out;                  // [T][d]
+  int act_bf16;
+};
+hipError_t launch_attn_paged(const AttnPagedArgs& a, hipStream_t st);
+
+// Tree attention: node i attends its root's shared prefix (paged) and its own
+// ancestor chain (node slots), then itself.
+struct AttnTreeArgs {
+  const void* qkv;             // [N][3d] new node tokens
+  const int32_t* root_of;      // [N]
+  const int32_t* block_table;  // [R][max_blocks] prefix blocks per root
+  const int32_t* prefix_len;   // [R]
+  const int32_t* anc_slot;     // [N][max_depth] pool slots of ancestors (root-side first), then self
+  const int32_t* n_anc;        // [N] entries used in anc_slot (ancestors + self)
+  const int32_t* group_start;  // [G+1] nodes grouped by root: tiles never straddle roots
+  int n_groups, max_blocks, max_depth, N, n_head, head_dim;
+  const void* pool;
+  float scale;
+  void* out;
+  int act_bf16;
+};
+hipError_t launch_attn_tree(const AttnTreeArgs& a, hipStream_t st);
+
+// ----------------------------------------------------------------- heads
+// logits/value/time from the heads GEMM output rows, plus softmax summary.
+struct HeadsArgs {
+  const float* z;        // [B][ldz] fp32 heads GEMM output (acc + bias)
+  int B, ldz, vocab, n_moves;
+  int value_col, time_col;
+  float temperature;     // the reference clamps it to >= 1e-5 (decode.py:191)
+  const uint32_t* legal; // optional [B][legal_words] bitmask over move ids
+  int legal_words;
+  float* logits;         // [B][vocab] or null
+  float* value;          // [B]
+  float* time;           // [B]
+  int32_t* top1;         // [B]
+  float* lse;            // [B] logsumexp of logits[:n_moves] * inv_temp (masked)
+  float* max_logit;      // [B]
+  int emulate_bf16;
+};
+hipError_t launch_heads(const HeadsArgs& a, hipStream_t st);
+
+// -------------------------------------------------------- weight packing
+// dst[n][k] = src[k][n] (Conv1D [in,out] -> [out,in]); bf16 or fp32 dst.
+hipError_t launch_transpose_convert(const float* src, int rows, int cols, void* dst, int dst_bf16,
+                                    int ld_dst, hipStream_t st);
+hipError_t launch_convert(const float* src, int64_t n, void* dst, int dst_bf16, int round_bf16,
+                          hipStream_t st);
+
+}  // namespace allie

@@ -1,0 +1,173 @@
+/*
+ * allie_amd -- C ABI of the MI355X (gfx950) engine for Allie's batched
+ * policy/value inference path.
+ *
+ * The reference (y0mingzhang/allie) is pure Python and has no FFI; its
+ * boundary is the model call `model(**batch) -> dict` of
+ * CausalLMWithRegressionHead.forward (src/modeling/model.py:85-147), fed by
+ * UCITokenizer.pad_and_collate (src/modeling/data.py:281-337) and read by the
+ * decode strategies at src/evaluation/decode.py:199-238,356-373.  Each entry
+ * point below names the part of that boundary it replaces.  The Python host
+ * side (allie_amd/capi.py) binds these symbols with ctypes.
+ *
+ * Conventions
+ *   - every pointer argument is device memory unless its name ends in _host;
+ *   - `stream` is a hipStream_t (torch.cuda.current_stream().cuda_stream);
+ *   - calls are stream-ordered, never synchronise the device and never
+ *     allocate device memory: the caller passes workspaces (sizes from the
+ *     *_workspace_bytes queries).  Only allie_model_create allocates (the
+ *     weight arena, freed by allie_model_destroy);
+ *   - return 0 on success or a negative ALLIE_ERR_* code; the message of the
+ *     last failure on the calling thread is allie_last_error().
+ */
+#ifndef ALLIE_AMD_H
+#define ALLIE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  ALLIE_OK = 0,
+  ALLIE_ERR_ARG = -1,        /* bad argument or shape */
+  ALLIE_ERR_HIP = -2,        /* a HIP runtime call failed */
+  ALLIE_ERR_NOMEM = -3,      /* weight arena allocation failed */
+  ALLIE_ERR_STATE = -4,      /* model not finalised / weight missing */
+  ALLIE_ERR_WORKSPACE = -5,  /* workspace too small */
+  ALLIE_ERR_LENGTH = -6      /* a game is empty or a table is too small */
+};
+
+/* Numeric modes. */
+enum {
+  ALLIE_MODE_FP32 = 0, /* fp32 weights and activations (fp32 check mode) */
+  ALLIE_MODE_BF16 = 1, /* bf16 GEMM operands, fp32 residual (torch autocast bf16) */
+  ALLIE_MODE_FP8W = 2  /* fp8 e4m3 per-output-channel weights, bf16 activations */
+};
+
+typedef struct allie_config {
+  int32_t n_layer, d_model, n_head, vocab_size, n_positions, max_length;
+  float eps;
+  int32_t mode;
+} allie_config;
+
+typedef struct allie_model allie_model;
+
+/* Weight kinds, in the reference's state-dict terms (see weights.py). */
+enum {
+  ALLIE_W_WTE = 0,   /* model.model.transformer.wte.weight [vocab][d]   */
+  ALLIE_W_WPE,       /* model.model.transformer.wpe.weight [n_pos][d]   */
+  ALLIE_W_CTRL,      /* model.control_embeds.weight [2][d]              */
+  ALLIE_W_LNF_G,     /* model.model.transformer.ln_f.weight [d]         */
+  ALLIE_W_LNF_B,
+  ALLIE_W_VALUE_W,   /* value_head.0.weight [1][d]                      */
+  ALLIE_W_VALUE_B,   /* value_head.0.bias [1]                           */
+  ALLIE_W_TIME_W,    /* time_head.0.weight [1][d]                       */
+  ALLIE_W_TIME_B,
+  ALLIE_W_LN1_G = 16,/* per layer: ...h.{i}.ln_1.weight [d]             */
+  ALLIE_W_LN1_B,
+  ALLIE_W_QKV_W,     /* ...attn.c_attn.weight [d][3d] (Conv1D in x out) */
+  ALLIE_W_QKV_B,
+  ALLIE_W_O_W,       /* ...attn.c_proj.weight [d][d]                    */
+  ALLIE_W_O_B,
+  ALLIE_W_LN2_G,
+  ALLIE_W_LN2_B,
+  ALLIE_W_FC_W,      /* ...mlp.c_fc.weight [d][4d]                      */
+  ALLIE_W_FC_B,
+  ALLIE_W_PR_W,      /* ...mlp.c_proj.weight [4d][d]                    */
+  ALLIE_W_PR_B
+};
+
+const char* allie_last_error(void);
+int allie_abi_version(void);
+
+/* Model lifetime.  Replaces initialize_model + load_state_dict
+ * (src/modeling/model.py:155-198, src/evaluation/evaluate.py:236-243). */
+int allie_model_create(const allie_config* cfg, allie_model** out);
+void allie_model_destroy(allie_model* m);
+/* src: fp32 tensor in the reference's layout (Conv1D weights [in][out]),
+ * rows x cols; converted and repacked into the model's arena. */
+int allie_model_set_weight(allie_model* m, int kind, int layer, const float* src, int64_t rows,
+                           int64_t cols, void* stream);
+/* fp8 mode only, for the four block GEMM weights: q [out][in] e4m3fn bytes,
+ * scale [out] fp32 (w[in][out] ~= q[out][in] * scale[out]). */
+int allie_model_set_weight_fp8(allie_model* m, int kind, int layer, const uint8_t* q,
+                               const float* scale, int64_t out_features, int64_t in_features,
+                               void* stream);
+/* Checks that every weight was set; required before any forward call. */
+int allie_model_finalize(allie_model* m);
+
+/* Ragged packing (replaces the padding half of pad_and_collate,
+ * src/modeling/data.py:281-337, for a flat word stream).
+ * words: games back to back; lens[n_seq]: words per game before the
+ * truncation to max_len (data.py:290).  Outputs are sized by the caller:
+ * cu_seqlens[n_seq+1], last_idx[n_seq], blk_off[n_seq+1],
+ * block_table[n_seq][max_blocks] (may be NULL), and ids/pos/seq_of/slot
+ * [capacity] (slot may be NULL).  in_off is int64 scratch [n_seq].
+ * status[1] is written 0 on success, else a bitmask: 1 empty game,
+ * 2 capacity exceeded (excess tokens dropped), 4 block table too small. */
+int allie_pack_ragged(const uint32_t* words, const int32_t* lens, int n_seq, int max_len,
+                      int block, int first_block, int max_blocks, int capacity,
+                      int32_t* cu_seqlens, int64_t* in_off, int32_t* ids, int32_t* pos,
+                      int32_t* seq_of, int32_t* last_idx, int32_t* blk_off,
+                      int32_t* block_table, int32_t* slot, int32_t* status, void* stream);
+
+/* Outputs of a forward, one entry per game (the values the decode
+ * strategies read from out["logits"][:, -1], out["value_logits"][:, -1],
+ * out["time_logits"][:, -1], decode.py:204-226). */
+typedef struct allie_outputs {
+  float* logits;     /* [n_seq][vocab] or NULL */
+  float* value;      /* [n_seq] tanh value head */
+  float* time;       /* [n_seq] time head (normalised units) */
+  int32_t* top1;     /* [n_seq] first argmax over (legal) move logits / T */
+  float* max_logit;  /* [n_seq] that maximum (of logits / T) */
+  float* lse;        /* [n_seq] logsumexp of (legal) move logits / T */
+} allie_outputs;
+
+/* Batched prefill forward: replaces `model(**pad_and_collate(games))` plus
+ * the last-token reads of Policy.score_full (decode.py:199-226).
+ * words: device word stream; lens_host: host array [n_seq].
+ * legal: optional [n_seq][legal_words] bitmask over move ids (NULL = all).
+ * kv_pool: optional paged KV pool of kv_pool_blocks blocks (layout
+ * [block][layer][k|v][head][16][head_dim], activation dtype) that receives
+ * every layer's keys and values; game i takes the contiguous blocks
+ * first_block + blk_off[i] ... (NULL = no cache). */
+size_t allie_prefill_workspace_bytes(const allie_model* m, int n_seq, int n_tokens);
+size_t allie_kv_block_bytes(const allie_model* m);
+int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_host, int n_seq,
+                  float temperature, const uint32_t* legal, int legal_words,
+                  const allie_outputs* out, void* kv_pool, int kv_pool_blocks, int first_block,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* Kernel probe for benchmarks: while active, every launch of one kernel kind
+ * inside allie_prefill is bracketed by HIP events on its stream;
+ * allie_probe_end waits for them and returns the summed duration.  Not
+ * re-entrant; the probed calls must all be on one device. */
+enum {
+  ALLIE_PROBE_QKV = 0,  /* QKV projection GEMM */
+  ALLIE_PROBE_PROJ,     /* attention output projection GEMM (+ residual) */
+  ALLIE_PROBE_FC,       /* MLP c_fc GEMM + gelu */
+  ALLIE_PROBE_FC2,      /* MLP c_proj GEMM (+ residual) */
+  ALLIE_PROBE_ATTN      /* varlen causal attention */
+};
+int allie_probe_begin(int kind, int max_launches);
+int allie_probe_end(float* total_ms_host, int* n_launches_host);
+
+/* Building blocks exported for tests and benchmarks.
+ * GEMM: C[m][n] (+)= sum_k A[m][k] W[n][k] with the engine's epilogues
+ * (0 store, 1 gelu, 2 residual add into R fp32); wtype 0 bf16, 1 fp32, 2 fp8. */
+int allie_gemm(const void* A, const void* W, const float* bias, const float* scale, void* C,
+               float* R, int M, int N, int K, int epi, int wtype, int out_f32, void* stream);
+int allie_attn_varlen(const void* qkv, const int32_t* cu_seqlens, const int32_t* tiles,
+                      int n_tiles, int n_seq, int n_tokens, int n_head, int head_dim,
+                      float scale, void* out, int act_bf16, void* stream);
+int allie_layernorm(const float* h, const int32_t* row_idx, int rows, int rows_out, int d,
+                    const float* g, const float* b, float eps, void* y, int act_bf16,
+                    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ALLIE_AMD_H */

@@ -1,0 +1,253 @@
+"""GPU parity of the individual kernels through the C ABI.
+
+* ragged packing: bit-exact against the C oracle (oracle/pack_ref.c);
+* GEMM (MFMA bf16 / fp8-weight / fp32): against torch fp32 matmuls of the
+  same (bf16-rounded) operands; bounds are half a bf16 ulp of the result
+  for rounded outputs and 1e-5 relative for fp32;
+* LayerNorm: against torch.nn.functional.layer_norm;
+* varlen causal attention: against a per-game fp32 softmax(q k^T / 8) v.
+"""
+import ctypes as C
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from allie_amd import capi
+from oracle import pack as opack
+
+pytestmark = pytest.mark.gpu
+
+L = None
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _lib(cuda):
+    global L
+    L = capi.lib()
+    yield
+
+
+def rb(x):
+    return x.to(torch.bfloat16).to(torch.float32)
+
+
+def dev_pack(words, lens, max_len=512, block=16, first_block=0, max_blocks=None, capacity=None):
+    dev = torch.device("cuda:0")
+    B = len(lens)
+    n = np.minimum(lens, max_len)
+    T = int(n.sum())
+    if max_blocks is None:
+        max_blocks = (max_len + block - 1) // block
+    cap = T if capacity is None else capacity
+    wd = torch.from_numpy(np.ascontiguousarray(words, dtype=np.uint32).view(np.int32)).to(dev)
+    ld = torch.from_numpy(np.asarray(lens, dtype=np.int32)).to(dev)
+    i32 = lambda k: torch.full((max(k, 1),), -7, dtype=torch.int32, device=dev)
+    out = {
+        "cu_seqlens": i32(B + 1), "ids": i32(cap), "pos": i32(cap), "seq_of": i32(cap),
+        "last_idx": i32(B), "blk_off": i32(B + 1), "block_table": i32(B * max_blocks),
+        "slot": i32(cap), "status": i32(1),
+    }
+    in_off = torch.empty(max(B, 1), dtype=torch.int64, device=dev)
+    rc = L.allie_pack_ragged(capi.ptr(wd), capi.ptr(ld), B, max_len, block, first_block, max_blocks, cap,
+                             capi.ptr(out["cu_seqlens"]), capi.ptr(in_off), capi.ptr(out["ids"]),
+                             capi.ptr(out["pos"]), capi.ptr(out["seq_of"]), capi.ptr(out["last_idx"]),
+                             capi.ptr(out["blk_off"]), capi.ptr(out["block_table"]), capi.ptr(out["slot"]),
+                             capi.ptr(out["status"]), capi.stream_ptr())
+    capi.check(rc, "pack")
+    torch.cuda.synchronize()
+    res = {k: v.cpu().numpy() for k, v in out.items()}
+    res["block_table"] = res["block_table"][: B * max_blocks].reshape(B, max_blocks)
+    for k in ("ids", "pos", "seq_of", "slot"):
+        res[k] = res[k][:cap]
+    res["cu_seqlens"] = res["cu_seqlens"][: B + 1]
+    return res
+
+
+def random_words(rng, lens):
+    T = int(np.sum(lens))
+    ids = rng.integers(0, 1997, T).astype(np.uint32)
+    outcome = rng.integers(0, 3, T).astype(np.uint32) << 14
+    secs = (rng.integers(0, 60, T).astype(np.uint32) + 1) << 16
+    return ids | outcome | secs
+
+
+@pytest.mark.parametrize("case", ["c2", "trunc", "single", "ones", "large_b"])
+def test_pack_bit_exact(case):
+    rng = np.random.default_rng(11)
+    if case == "c2":
+        lens = np.random.default_rng(2).integers(8, 401, 256).astype(np.int32)
+    elif case == "trunc":
+        lens = rng.integers(400, 700, 37).astype(np.int32)
+    elif case == "single":
+        lens = np.array([5], np.int32)
+    elif case == "ones":
+        lens = np.ones(1500, np.int32)
+    else:
+        lens = rng.integers(1, 80, 3000).astype(np.int32)
+    words = random_words(rng, lens)
+    got = dev_pack(words, lens, first_block=3)
+    ref = opack.pack(words, lens, first_block=3)
+    assert got["status"][0] == 0
+    for k in ("cu_seqlens", "ids", "pos", "seq_of", "last_idx", "blk_off", "block_table", "slot"):
+        np.testing.assert_array_equal(got[k], ref[k], err_msg=k)
+
+
+def test_pack_status_flags():
+    rng = np.random.default_rng(5)
+    lens = np.array([4, 0, 6], np.int32)
+    words = random_words(rng, lens)
+    got = dev_pack(words, lens)
+    assert got["status"][0] & 1
+    lens = np.array([40, 50], np.int32)
+    words = random_words(rng, lens)
+    got = dev_pack(words, lens, capacity=60)  # too small: excess dropped, flagged
+    assert got["status"][0] & 2
+    assert (got["ids"][:40] == (words[:40] & 0x3FFF)).all()
+    got = dev_pack(words, lens, max_blocks=2)  # 40 tokens need 3 blocks of 16
+    assert got["status"][0] & 4
+
+
+def _gemm(A, Wt, bias, epi, wtype, out_f32=False, R=None, scale=None):
+    M, K = A.shape
+    N = Wt.shape[0]
+    dev = A.device
+    if epi == capi.EPI_RESID:
+        C_ = None
+    elif out_f32 or wtype == capi.WT_F32:
+        C_ = torch.empty(M, N, dtype=torch.float32, device=dev)
+    else:
+        C_ = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    rc = L.allie_gemm(capi.ptr(A), capi.ptr(Wt), capi.ptr(bias), capi.ptr(scale), capi.ptr(C_), capi.ptr(R),
+                      M, N, K, epi, wtype, int(out_f32), capi.stream_ptr())
+    capi.check(rc, "gemm")
+    torch.cuda.synchronize()
+    return C_
+
+
+SHAPES = [(1, 256, 64), (300, 768, 256), (777, 1024, 1024), (1000, 3072, 1024), (513, 1024, 4096), (64, 4096, 1024)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_bf16_epilogues(M, N, K, cuda):
+    g = torch.Generator(device="cpu").manual_seed(M * 7 + N + K)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16).to(cuda)
+    Wt = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16).to(cuda)
+    b = rb(torch.randn(N, generator=g) * 0.1).to(cuda)
+    acc = A.float() @ Wt.float().T + b
+    # store
+    C_ = _gemm(A, Wt, b, capi.EPI_STORE, capi.WT_BF16).float()
+    assert ((C_ - acc).abs() <= acc.abs() * 2 ** -8 + 1e-5).all()
+    # fp32 output (heads)
+    C32 = _gemm(A, Wt, b, capi.EPI_STORE, capi.WT_BF16, out_f32=True)
+    torch.testing.assert_close(C32, acc, rtol=1e-5, atol=1e-4)
+    # gelu
+    Cg = _gemm(A, Wt, b, capi.EPI_GELU, capi.WT_BF16).float()
+    t = rb(acc)
+    ref = (0.5 * t) * (1 + torch.tanh(math.sqrt(2 / math.pi) * (t + 0.044715 * t ** 3)))
+    assert ((Cg - ref).abs() <= ref.abs() * 2 ** -6 + 2e-3).all()
+    # residual
+    R0 = torch.randn(M, N, generator=g).to(cuda)
+    R = R0.clone()
+    _gemm(A, Wt, b, capi.EPI_RESID, capi.WT_BF16, R=R)
+    assert ((R - (R0 + acc)).abs() <= acc.abs() * 2 ** -8 + 1e-5).all()
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 768, 256), (1000, 3072, 1024)])
+def test_gemm_fp8_weights(M, N, K, cuda):
+    g = torch.Generator(device="cpu").manual_seed(N + K)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16).to(cuda)
+    w = torch.randn(N, K, generator=g) * 0.05
+    s = (w.abs().amax(1) / 448.0).float()
+    q = (w / s[:, None]).to(torch.float8_e4m3fn)
+    deq = q.float() * s[:, None]
+    b = rb(torch.randn(N, generator=g) * 0.1).to(cuda)
+    qd, sd = q.view(torch.uint8).to(cuda), s.to(cuda)
+    acc = A.float() @ deq.to(cuda).T + b
+    C_ = _gemm(A, qd, b, capi.EPI_STORE, capi.WT_FP8, scale=sd).float()
+    assert ((C_ - acc).abs() <= acc.abs() * 2 ** -8 + 1e-4).all()
+    R0 = torch.randn(M, N, generator=g).to(cuda)
+    R = R0.clone()
+    _gemm(A, qd, b, capi.EPI_RESID, capi.WT_FP8, R=R, scale=sd)
+    assert ((R - (R0 + acc)).abs() <= acc.abs() * 2 ** -8 + 1e-4).all()
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 256, 64), (300, 770, 256), (129, 2048, 1024)])
+def test_gemm_fp32(M, N, K, cuda):
+    g = torch.Generator(device="cpu").manual_seed(N * 3 + K)
+    A = torch.randn(M, K, generator=g).to(cuda)
+    Wt = (torch.randn(N, K, generator=g) * 0.05).to(cuda)
+    b = (torch.randn(N, generator=g) * 0.1).to(cuda)
+    acc = (A.double() @ Wt.double().T + b.double()).float()
+    C_ = _gemm(A, Wt, b, capi.EPI_STORE, capi.WT_F32)
+    torch.testing.assert_close(C_, acc, rtol=1e-5, atol=1e-5)
+    Cg = _gemm(A, Wt, b, capi.EPI_GELU, capi.WT_F32)
+    torch.testing.assert_close(Cg, torch.nn.functional.gelu(acc, approximate="tanh"), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+def test_layernorm(bf16, cuda):
+    g = torch.Generator(device="cpu").manual_seed(3)
+    d = 1024
+    h = (torch.randn(100, d, generator=g) * 3 + 1).to(cuda)
+    gam = (1 + 0.1 * torch.randn(d, generator=g)).to(cuda)
+    bet = (0.1 * torch.randn(d, generator=g)).to(cuda)
+    idx = torch.tensor([5, 99, 0, 42], dtype=torch.int32, device=cuda)
+    y = torch.empty(6, d, dtype=torch.bfloat16 if bf16 else torch.float32, device=cuda)
+    rc = L.allie_layernorm(capi.ptr(h), capi.ptr(idx), 4, 6, d, capi.ptr(gam), capi.ptr(bet), 1e-5, capi.ptr(y),
+                           int(bf16), capi.stream_ptr())
+    capi.check(rc)
+    torch.cuda.synchronize()
+    ref = torch.nn.functional.layer_norm(h[idx.long()], (d,), gam, bet, 1e-5)
+    tol = 2 ** -8 if bf16 else 1e-5
+    assert ((y[:4].float() - ref).abs() <= ref.abs() * tol + 1e-5).all()
+    assert (y[4:].float() == 0).all()
+
+
+def _tiles(lens, qt=64):
+    nt = [(n + qt - 1) // qt for n in lens]
+    out = []
+    for q in range(max(nt) - 1, -1, -1):
+        out += [(s << 5) | q for s in range(len(lens)) if nt[s] > q]
+    return out
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+@pytest.mark.parametrize("H", [4, 16])
+def test_attention_varlen(bf16, H, cuda):
+    lens = [1, 2, 5, 31, 32, 33, 63, 64, 65, 127, 128, 129, 200, 300, 400, 511, 512]
+    if H == 16 and not bf16:
+        lens = lens[:12]
+    d = H * 64
+    T = sum(lens)
+    g = torch.Generator(device="cpu").manual_seed(H)
+    qkv = torch.randn(T, 3 * d, generator=g) * 1.5
+    if bf16:
+        qkv = rb(qkv)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    tiles = _tiles(lens)
+    dt = torch.bfloat16 if bf16 else torch.float32
+    qkv_d = qkv.to(dt).to(cuda)
+    out = torch.full((T, d), float("nan"), dtype=dt, device=cuda)
+    cu_d = torch.from_numpy(cu).to(cuda)
+    tiles_d = torch.tensor(tiles, dtype=torch.int32, device=cuda)
+    rc = L.allie_attn_varlen(capi.ptr(qkv_d), capi.ptr(cu_d), capi.ptr(tiles_d), len(tiles), len(lens), T, H, 64,
+                             0.125, capi.ptr(out), int(bf16), capi.stream_ptr())
+    capi.check(rc)
+    torch.cuda.synchronize()
+    out = out.float().cpu()
+    for s, n in enumerate(lens):
+        x = qkv[cu[s]: cu[s + 1]]
+        q, k, v = x.split(d, dim=1)
+        q = q.view(n, H, 64).transpose(0, 1)
+        k = k.view(n, H, 64).transpose(0, 1)
+        v = v.view(n, H, 64).transpose(0, 1)
+        sc = (q @ k.transpose(1, 2)) * 0.125
+        sc = sc.masked_fill(~torch.ones(n, n, dtype=torch.bool).tril(), float("-inf"))
+        ref = (torch.softmax(sc, -1) @ v).transpose(0, 1).reshape(n, d)
+        got = out[cu[s]: cu[s + 1]]
+        if bf16:
+            torch.testing.assert_close(got, ref, rtol=2e-2, atol=2e-2)
+        else:
+            torch.testing.assert_close(got, ref, rtol=1e-5, atol=1e-5)

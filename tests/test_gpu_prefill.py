@@ -1,0 +1,126 @@
+"""End-to-end parity of the batched prefill against the CPU oracle.
+
+Bars (from the path's contract):
+* fp32 check mode: logits, value and time within 1e-4 of the fp32 oracle and
+  the top-1 move identical;
+* bf16 mode: within 2e-2 of the oracle's bf16-autocast emulation; top-1
+  identical on every game whose oracle top-2 margin exceeds twice the
+  observed logit error (closer calls are counted and reported);
+* fp8-weight mode: within 2e-2 of the oracle's fp8w mode, same top-1 rule.
+"""
+import numpy as np
+import pytest
+import torch
+
+from allie_amd import config, weights
+from allie_amd.engine import Engine, legal_mask
+from oracle.model_ref import RefModel, policy_summary
+
+pytestmark = pytest.mark.gpu
+
+
+def synth_games(seed, B, lo, hi, elo=False):
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(lo, hi + 1, B).astype(np.int32)
+    seqs = []
+    for n in lens:
+        s = rng.integers(0, 1968, n).astype(np.uint32)
+        if elo and n >= 3:
+            s[0] = 1997 + int(rng.integers(400, 3200))
+            s[1] = 1997 + int(rng.integers(400, 3200))
+            s[2] = 1968 + int(rng.integers(0, 24))
+        s |= (rng.integers(0, 3, n).astype(np.uint32) << 14) | ((rng.integers(0, 30, n).astype(np.uint32) + 1) << 16)
+        seqs.append(s)
+    return seqs, lens
+
+
+def run_engine(eng, seqs, lens, **kw):
+    words = np.concatenate(seqs)
+    r = eng.prefill(words, lens, **kw)
+    torch.cuda.synchronize()
+    return {k: (v.cpu().numpy() if v is not None else None) for k, v in r.__dict__.items()}
+
+
+def check(got, ref, tol, mode):
+    dl = np.abs(got["logits"] - ref["logits"]).max()
+    dv = np.abs(got["value"] - ref["value_logits"]).max()
+    dt = np.abs(got["time"] - ref["time_logits"]).max()
+    assert dl <= tol and dv <= tol and dt <= tol, (mode, dl, dv, dt)
+    ps = policy_summary(ref["logits"])
+    need = ps["margin"] > max(2 * dl, 1e-6)
+    assert (got["top1"][need] == ps["top1"][need]).all(), (mode, np.nonzero(got["top1"] != ps["top1"]))
+    # lse of the move logits
+    np.testing.assert_allclose(got["lse"], ps["lse"], atol=max(tol, 2 * dl) * 2)
+    return int((~need).sum())
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    cfg = config.TINY
+    sd = weights.init_weights(cfg, seed=7, perturb=True)
+    return cfg, sd
+
+
+@pytest.mark.parametrize("mode,tol", [("float32", 1e-4), ("bfloat16", 2e-2), ("fp8w", 2e-2)])
+def test_prefill_tiny_perturbed(tiny, mode, tol, cuda):
+    cfg, sd = tiny
+    seqs, lens = synth_games(1, 23, 1, 150, elo=True)
+    seqs.append(np.arange(600, dtype=np.uint32) % 1968)  # truncated to the first 512 words
+    lens = np.append(lens, 600).astype(np.int32)
+    eng = Engine(cfg, sd, mode=mode)
+    got = run_engine(eng, seqs, lens)
+    ref = RefModel(cfg, sd, mode=mode).forward_last([(s & 0x3FFF)[:512].astype(np.int64) for s in seqs])
+    check(got, ref, tol, mode)
+    eng.close()
+
+
+def test_prefill_legal_mask_and_temperature(tiny, cuda):
+    cfg, sd = tiny
+    seqs, lens = synth_games(3, 9, 5, 60)
+    eng = Engine(cfg, sd, mode="float32")
+    rng = np.random.default_rng(0)
+    legal = [sorted(rng.choice(1968, size=int(rng.integers(1, 40)), replace=False).tolist()) for _ in lens]
+    got = run_engine(eng, seqs, lens, legal=legal_mask(legal), temperature=0.7)
+    ref = RefModel(cfg, sd).forward_last([(s & 0x3FFF).astype(np.int64) for s in seqs])
+    for b, ids in enumerate(legal):
+        l = ref["logits"][b, ids].astype(np.float64) / 0.7
+        assert got["top1"][b] == ids[int(np.argmax(l))]
+        m = l.max()
+        np.testing.assert_allclose(got["lse"][b], m + np.log(np.exp(l - m).sum()), atol=1e-4)
+    eng.close()
+
+
+def test_prefill_small_c1(cuda):
+    """C1 shape (12 x 768), fp32 check mode, 8 prefixes of 20..120 tokens."""
+    cfg = config.SMALL
+    sd = weights.init_weights(cfg, seed=0)
+    rng = np.random.default_rng(1)
+    lens = rng.integers(20, 121, 8).astype(np.int32)
+    seqs = [rng.integers(0, 1968, n).astype(np.uint32) for n in lens]
+    eng = Engine(cfg, sd, mode="float32")
+    got = run_engine(eng, seqs, lens)
+    ref = RefModel(cfg, sd).forward_last([s.astype(np.int64) for s in seqs])
+    check(got, ref, 1e-4, "c1-fp32")
+    eng.close()
+
+
+@pytest.fixture(scope="module")
+def medium():
+    cfg = config.MEDIUM
+    return cfg, weights.init_weights(cfg, seed=0)
+
+
+def test_prefill_medium_c2_subset(medium, cuda):
+    """C2 (medium, bf16, 256 prefixes of 8..400): the full batch runs on the
+    GPU; 10 of its games are checked against the oracle's bf16 emulation."""
+    cfg, sd = medium
+    rng = np.random.default_rng(2)
+    lens = rng.integers(8, 401, 256).astype(np.int32)
+    seqs = [rng.integers(0, 1968, n).astype(np.uint32) for n in lens]
+    eng = Engine(cfg, sd, mode="bfloat16")
+    got = run_engine(eng, seqs, lens)
+    pick = [0, 1, 2, 3, int(np.argmax(lens)), int(np.argmin(lens)), 100, 200, 254, 255]
+    ref = RefModel(cfg, sd, mode="bfloat16").forward_last([seqs[i].astype(np.int64) for i in pick])
+    sub = {k: (v[pick] if v is not None else None) for k, v in got.items()}
+    check(sub, ref, 2e-2, "c2-bf16")
+    eng.close()
