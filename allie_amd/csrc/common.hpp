@@ -55,7 +55,17 @@ ALLIE_DEV float tanh_fast(float x) {
   return 1.0f - 2.0f / (e + 1.0f);
 }
 
-// gelu_new (tanh form), evaluated in fp32.
+// gelu_new for the bf16 epilogues: 0.5 x (1 + tanh(u)) == x * sigmoid(2 u)
+// with u = sqrt(2/pi) (x + 0.044715 x^3); hardware exp2 and reciprocal
+// (relative error ~1e-7, far below the bf16 rounding of the result).
+ALLIE_DEV float gelu_tanh_fast(float x) {
+  const float k2 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;  // -2 sqrt(2/pi) log2(e)
+  const float u = x + 0.044715f * (x * x * x);
+  const float e = __builtin_amdgcn_exp2f(k2 * u);
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// gelu_new (tanh form), evaluated in fp32 with the precise tanh (fp32 path).
 ALLIE_DEV float gelu_tanh(float x) {
   const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
   float inner = k0 * (x + 0.044715f * (x * x * x));

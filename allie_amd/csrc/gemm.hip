@@ -7,7 +7,9 @@
 // weights repacked once to [out][in] at load time.
 //
 // MFMA kernel: 256 threads (4 waves, 2 x 2), block tile 256 (M) x 256 (N),
-// BK = 64, register-staged double-buffered LDS (2 x 64 KiB), one block per CU.
+// BK = 64, double-buffered LDS (2 x 64 KiB) filled by direct global->LDS
+// 16-byte loads (fp8 weights go through registers to be widened to bf16),
+// one block per CU.
 // Each wave owns a 128 x 128 sub-tile = 4 x 4 MFMA 32x32x16 bf16 blocks
 // (256 fp32 accumulators).  The MFMA's first operand is the weight fragment
 // and its second the activation fragment, so each lane's accumulator holds 4
@@ -55,81 +57,65 @@ ALLIE_DEV void tile_coords(int pid, int G, int num_tm, int num_tn, int& tm, int&
   tn = in_group / gm;
 }
 
+// fp8 weight tile (256 rows x 64 e4m3, register staged: 4 x 16 bytes per
+// thread) -> bf16 into the swizzled LDS layout.
+ALLIE_DEV void fp8_tile_to_lds(const uint4* rw, bf16_t* sw, int tid) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = (tid >> 2) + 64 * i;
+    const uint32_t w4[4] = {rw[i].x, rw[i].y, rw[i].z, rw[i].w};
+    uint32_t o[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t v = w4[j];
+      o[2 * j] = fp8e4m3_to_bf16(v & 0xffu) | (fp8e4m3_to_bf16((v >> 8) & 0xffu) << 16);
+      o[2 * j + 1] = fp8e4m3_to_bf16((v >> 16) & 0xffu) | (fp8e4m3_to_bf16(v >> 24) << 16);
+    }
+    const int c = (tid & 3) * 2;
+    *reinterpret_cast<uint4*>(&sw[swz(row, c)]) = make_uint4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<uint4*>(&sw[swz(row, c + 1)]) = make_uint4(o[4], o[5], o[6], o[7]);
+  }
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Direct global -> LDS copy of 16 bytes per lane: the wave writes 1 KiB of
+// LDS contiguously at `lds` (lane i at lds + 16 i).
+ALLIE_DEV void g2l_16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void_t*)lds, 16, 0, 0);
+}
+ALLIE_DEV void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 template <int EPI, int WT, bool OUT_F32>
 __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) bf16_t sA[2][BM * BK];
-  __shared__ __attribute__((aligned(16))) bf16_t sW[2][BN * BK];
+  __shared__ __attribute__((aligned(1024))) bf16_t sA[2][BM * BK];
+  __shared__ __attribute__((aligned(1024))) bf16_t sW[2][BN * BK];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (LDS-DMA base)
   const int num_tm = (a.M + BM - 1) / BM, num_tn = a.N / BN;
   int tm, tn;
   tile_coords(blockIdx.x, gridDim.x, num_tm, num_tn, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int K = a.K;
-
   const bf16_t* __restrict__ A = reinterpret_cast<const bf16_t*>(a.A);
-  // ---- global -> register staging ---------------------------------------
-  // A tile: 256 rows x 8 chunks; thread loads chunk (tid & 7) of rows
-  // (tid >> 3) + 32 i.
-  const int lc = tid & 7, lr = tid >> 3;
-  const bf16_t* a_src[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    int m = m0 + lr + 32 * i;
-    m = m < a.M ? m : a.M - 1;
-    a_src[i] = A + (int64_t)m * a.lda + lc * 8;
-  }
-  uint4 ra[8];
-  constexpr int WCH = (WT == W_FP8) ? 4 : 8;  // 16-byte global chunks per thread
-  uint4 rw[WCH];
-  const bf16_t* __restrict__ Wb = reinterpret_cast<const bf16_t*>(a.W);
-  const uint8_t* __restrict__ W8 = reinterpret_cast<const uint8_t*>(a.W);
 
-  auto load_global = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ra[i] = *reinterpret_cast<const uint4*>(a_src[i] + k0);
-    if constexpr (WT == W_FP8) {
-      // W tile: 256 rows x 4 chunks of 16 fp8; thread loads chunk (tid & 3) of
-      // rows (tid >> 2) + 64 i.
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = (tid >> 2) + 64 * i;
-        rw[i] = *reinterpret_cast<const uint4*>(W8 + (int64_t)(n0 + row) * K + k0 + (tid & 3) * 16);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int row = lr + 32 * i;
-        rw[i] = *reinterpret_cast<const uint4*>(Wb + (int64_t)(n0 + row) * K + k0 + lc * 8);
-      }
-    }
-  };
-  auto store_lds = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      *reinterpret_cast<uint4*>(&sA[buf][swz(lr + 32 * i, lc)]) = ra[i];
-    if constexpr (WT == W_FP8) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = (tid >> 2) + 64 * i;
-        const uint32_t w4[4] = {rw[i].x, rw[i].y, rw[i].z, rw[i].w};
-        uint32_t o[8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t v = w4[j];
-          o[2 * j] = fp8e4m3_to_bf16(v & 0xffu) | (fp8e4m3_to_bf16((v >> 8) & 0xffu) << 16);
-          o[2 * j + 1] = fp8e4m3_to_bf16((v >> 16) & 0xffu) | (fp8e4m3_to_bf16(v >> 24) << 16);
-        }
-        const int c = (tid & 3) * 2;
-        *reinterpret_cast<uint4*>(&sW[buf][swz(row, c)]) = make_uint4(o[0], o[1], o[2], o[3]);
-        *reinterpret_cast<uint4*>(&sW[buf][swz(row, c + 1)]) = make_uint4(o[4], o[5], o[6], o[7]);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        *reinterpret_cast<uint4*>(&sW[buf][swz(lr + 32 * i, lc)]) = rw[i];
-    }
-  };
+  // Loader geometry: wave w fills rows [64 w, 64 w + 64) of each tile with 8
+  // LDS-DMA instructions of 8 rows; lane -> (row 8 i + lane / 8, physical
+  // chunk lane % 8), reading logical chunk (lane % 8) ^ (row & 7).
+  const int lr = lane >> 3, pc = lane & 7, lcg = pc ^ lr;
+  // rows of this lane: m0 + 64 wave + 8 i + lr (i = 0..7); rows at or past M
+  // read the last valid row instead (their results are discarded)
+  const int m_first = m0 + wave * 64 + lr;
+  const int m_last_ok = a.M - 1 - m_first;  // copy i is in range iff 8 i <= m_last_ok
+  const bf16_t* a_row0 = A + (int64_t)(m_first < a.M ? m_first : a.M - 1) * a.lda + lcg * 8;
+  const bf16_t* a_last = A + (int64_t)(a.M - 1) * a.lda + lcg * 8;
+  const int64_t a_step = (int64_t)8 * a.lda;
+  const bf16_t* __restrict__ Wb = reinterpret_cast<const bf16_t*>(a.W);
+  const bf16_t* w_row0 = Wb + (int64_t)(n0 + wave * 64 + lr) * K + lcg * 8;
+  const int64_t w_step = (int64_t)8 * K;
+  const uint8_t* __restrict__ W8 = reinterpret_cast<const uint8_t*>(a.W);
+  uint4 rw[4];
 
   f32x16_t acc[4][4];
 #pragma unroll
@@ -139,14 +125,48 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs a) {
 
   const int wm = wave & 1, wn = wave >> 1;
   const int frow = lane & 31, fgrp = lane >> 5;
-
-  load_global(0);
-  store_lds(0);
-  __syncthreads();
   const int KT = K / BK;
+
+#define ISSUE_A(buf, k0)                                                              \
+  _Pragma("unroll") for (int i = 0; i < 8; ++i) {                                     \
+    const bf16_t* src = (8 * i <= m_last_ok) ? a_row0 + (int64_t)i * a_step : a_last; \
+    g2l_16(src + (k0), &sA[buf][(wave * 64 + 8 * i) * BK]);                           \
+  }
+#define ISSUE_W(buf, k0)                                                              \
+  _Pragma("unroll") for (int i = 0; i < 8; ++i)                                       \
+    g2l_16(w_row0 + (int64_t)i * w_step + (k0), &sW[buf][(wave * 64 + 8 * i) * BK]);
+
+  // ---- prologue: stage tile 0 ---------------------------------------------
+  ISSUE_A(0, 0);
+  if constexpr (WT == W_FP8) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = (tid >> 2) + 64 * i;
+      rw[i] = *reinterpret_cast<const uint4*>(W8 + (int64_t)(n0 + row) * K + (tid & 3) * 16);
+    }
+  } else {
+    ISSUE_W(0, 0);
+  }
+  if constexpr (WT == W_FP8) fp8_tile_to_lds(rw, &sW[0][0], tid);
+  wait_vmem();
+  __syncthreads();
+
   for (int kt = 0; kt < KT; ++kt) {
     const int buf = kt & 1;
-    if (kt + 1 < KT) load_global((kt + 1) * BK);
+    const bool more = kt + 1 < KT;
+    if (more) {
+      const int k1 = (kt + 1) * BK;
+      ISSUE_A(buf ^ 1, k1);
+      if constexpr (WT == W_FP8) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = (tid >> 2) + 64 * i;
+          rw[i] = *reinterpret_cast<const uint4*>(W8 + (int64_t)(n0 + row) * K + k1 + (tid & 3) * 16);
+        }
+      } else {
+        ISSUE_W(buf ^ 1, k1);
+      }
+    }
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
       const int c = kk * 2 + fgrp;
@@ -164,9 +184,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs a) {
         for (int j = 0; j < 4; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], xf[j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < KT) store_lds(buf ^ 1);
+    if constexpr (WT == W_FP8) {
+      if (more) fp8_tile_to_lds(rw, &sW[buf ^ 1][0], tid);
+    }
+    wait_vmem();
     __syncthreads();
   }
+#undef ISSUE_A
+#undef ISSUE_W
 
   // ---- epilogue ------------------------------------------------------------
 #pragma unroll
@@ -186,10 +211,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs a) {
         float v2 = acc[i][j][q * 4 + 2] * scl.z + bias.z;
         float v3 = acc[i][j][q * 4 + 3] * scl.w + bias.w;
         if constexpr (EPI == EPI_GELU) {
-          v0 = gelu_tanh(round_bf16(v0));
-          v1 = gelu_tanh(round_bf16(v1));
-          v2 = gelu_tanh(round_bf16(v2));
-          v3 = gelu_tanh(round_bf16(v3));
+          v0 = gelu_tanh_fast(round_bf16(v0));
+          v1 = gelu_tanh_fast(round_bf16(v1));
+          v2 = gelu_tanh_fast(round_bf16(v2));
+          v3 = gelu_tanh_fast(round_bf16(v3));
         }
         if constexpr (EPI == EPI_RESID) {
           float4* r = reinterpret_cast<float4*>(a.R + (int64_t)m * a.ldr + n);
