@@ -380,7 +380,8 @@ int allie_pack_ragged(const uint32_t* words, const int32_t* lens, int n_seq, int
                       int block, int first_block, int max_blocks, int capacity,
                       int32_t* cu_seqlens, int64_t* in_off, int32_t* ids, int32_t* pos,
                       int32_t* seq_of, int32_t* last_idx, int32_t* blk_off,
-                      int32_t* block_table, int32_t* slot, int32_t* status, void* stream) {
+                      int32_t* block_table, int32_t* slot, int pad_id, int32_t* status,
+                      void* stream) {
   if (n_seq < 0 || max_len <= 0 || block <= 0 || max_blocks < 0 || capacity < 0)
     return fail(ALLIE_ERR_ARG, "bad pack sizes");
   if (!lens || !cu_seqlens || !in_off || !last_idx || !blk_off || !status ||
@@ -406,6 +407,7 @@ int allie_pack_ragged(const uint32_t* words, const int32_t* lens, int n_seq, int
   p.block_table = block_table;
   p.slot = slot;
   p.tiles = nullptr;
+  p.pad_id = pad_id;
   p.status = status;
   HIP_TRY(launch_pack(p, (hipStream_t)stream));
   return ALLIE_OK;
@@ -473,6 +475,7 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
   p.block_table = nullptr;
   p.slot = kv_pool ? w.slot : nullptr;
   p.tiles = w.tiles;
+  p.pad_id = ALLIE_PAD_ID;
   p.status = w.status;
   HIP_TRY(launch_pack(p, st));
 

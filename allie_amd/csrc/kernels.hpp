@@ -21,7 +21,9 @@ struct PackArgs {
   int32_t* block_table;   // [B][max_blocks] or null
   int32_t* slot;          // [T] or null
   int32_t* tiles;         // attention query tiles or null
-  int32_t* status;        // [1]: bit 1 empty game, 2 capacity exceeded, 4 table too small
+  int pad_id;             // token id flagged when it occurs inside a game (-1: none)
+  int32_t* status;        // [1]: bit 1 empty game, 2 capacity exceeded, 4 table too small,
+                          //      8 PAD id inside a game
 };
 hipError_t launch_pack(const PackArgs& a, hipStream_t st);
 

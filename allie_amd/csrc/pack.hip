@@ -121,9 +121,9 @@ __global__ __launch_bounds__(256) void pack_fill_kernel(
     int block, int first_block, int max_blocks, const int32_t* __restrict__ cu_seqlens,
     const int64_t* __restrict__ in_off, const int32_t* __restrict__ blk_off,
     int32_t* __restrict__ ids, int32_t* __restrict__ pos, int32_t* __restrict__ seq_of,
-    int32_t* __restrict__ block_table, int32_t* __restrict__ slot, int capacity) {
+    int32_t* __restrict__ block_table, int32_t* __restrict__ slot, int capacity, int pad_id,
+    int32_t* __restrict__ status) {
   const int s = blockIdx.x;
-  if (s >= B) return;
   int n = lens[s] < max_len ? lens[s] : max_len;
   if (n < 0) n = 0;
   const int t0 = cu_seqlens[s];
@@ -134,13 +134,19 @@ __global__ __launch_bounds__(256) void pack_fill_kernel(
     for (int j = threadIdx.x; j < max_blocks; j += blockDim.x)
       block_table[(int64_t)s * max_blocks + j] = j < nb ? b0 + j : -1;
   const int n_fit = t0 + n <= capacity ? n : (capacity > t0 ? capacity - t0 : 0);
+  int pad_seen = 0;
   for (int j = threadIdx.x; j < n_fit; j += blockDim.x) {
     uint32_t w = words[w0 + j];
-    ids[t0 + j] = (int32_t)(w & 0x3FFFu);
+    const int32_t id = (int32_t)(w & 0x3FFFu);
+    pad_seen |= id == pad_id;
+    ids[t0 + j] = id;
     pos[t0 + j] = j;
     seq_of[t0 + j] = s;
     if (slot != nullptr) slot[t0 + j] = (b0 + j / block) * block + j % block;
   }
+  // a PAD id inside a game would be a masked key in the reference's padded
+  // batch (data.py:321) but is an ordinary token here: flag it
+  if (__syncthreads_or(pad_seen) && threadIdx.x == 0 && status != nullptr) atomicOr(status, 8);
 }
 
 }  // namespace
@@ -156,7 +162,8 @@ hipError_t launch_pack(const PackArgs& a, hipStream_t st) {
   if (a.B > 0) {
     hipLaunchKernelGGL(pack_fill_kernel, dim3(a.B), dim3(256), 0, st, a.words, a.lens, a.B,
                        a.max_len, a.block, a.first_block, a.max_blocks, a.cu_seqlens, a.in_off,
-                       a.blk_off, a.ids, a.pos, a.seq_of, a.block_table, a.slot, a.capacity);
+                       a.blk_off, a.ids, a.pos, a.seq_of, a.block_table, a.slot, a.capacity,
+                       a.pad_id, a.status);
     e = hipGetLastError();
   }
   return e;

@@ -40,6 +40,10 @@ enum {
   ALLIE_ERR_LENGTH = -6      /* a game is empty or a table is too small */
 };
 
+/* Token id of <PAD> (src/modeling/data.py:197-198: moves, 24 time
+ * controls, the resign token, then <BOS> <EOS> <UNK> <PAD>). */
+#define ALLIE_PAD_ID 1996
+
 /* Numeric modes. */
 enum {
   ALLIE_MODE_FP32 = 0, /* fp32 weights and activations (fp32 check mode) */
@@ -107,12 +111,15 @@ int allie_model_finalize(allie_model* m);
  * block_table[n_seq][max_blocks] (may be NULL), and ids/pos/seq_of/slot
  * [capacity] (slot may be NULL).  in_off is int64 scratch [n_seq].
  * status[1] is written 0 on success, else a bitmask: 1 empty game,
- * 2 capacity exceeded (excess tokens dropped), 4 block table too small. */
+ * 2 capacity exceeded (excess tokens dropped), 4 block table too small,
+ * 8 the id pad_id occurs inside a game (pass -1 to skip the check; the
+ * reference would mask such a token, data.py:321, the packer keeps it). */
 int allie_pack_ragged(const uint32_t* words, const int32_t* lens, int n_seq, int max_len,
                       int block, int first_block, int max_blocks, int capacity,
                       int32_t* cu_seqlens, int64_t* in_off, int32_t* ids, int32_t* pos,
                       int32_t* seq_of, int32_t* last_idx, int32_t* blk_off,
-                      int32_t* block_table, int32_t* slot, int32_t* status, void* stream);
+                      int32_t* block_table, int32_t* slot, int pad_id, int32_t* status,
+                      void* stream);
 
 /* Outputs of a forward, one entry per game (the values the decode
  * strategies read from out["logits"][:, -1], out["value_logits"][:, -1],

@@ -10,6 +10,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB = os.path.join(_HERE, "_build", "liboracle.so")
 _lib = None
+PAD_ID = 1996
 
 
 def build() -> str:
@@ -32,12 +33,14 @@ def _p(a):
 
 
 def pack(words: np.ndarray, lens: np.ndarray, max_len: int = 512, block: int = 16,
-         first_block: int = 0, max_blocks: int | None = None) -> dict:
+         first_block: int = 0, max_blocks: int | None = None, pad_id: int = PAD_ID) -> dict:
+    """Packed layout of ``words``/``lens``; ``out["status"]`` has the engine's
+    status bits (1 empty game, 4 table too small, 8 PAD id inside a game)."""
     lib = _load()
     words = np.ascontiguousarray(words, dtype=np.uint32)
     lens = np.ascontiguousarray(lens, dtype=np.int32)
     B = len(lens)
-    n = np.minimum(lens, max_len)
+    n = np.clip(lens, 0, max_len)
     T = int(n.sum())
     if max_blocks is None:
         max_blocks = (max_len + block - 1) // block
@@ -51,10 +54,9 @@ def pack(words: np.ndarray, lens: np.ndarray, max_len: int = 512, block: int = 1
         "block_table": np.zeros((B, max_blocks), np.int32),
         "slot": np.zeros(T, np.int32),
     }
-    rc = lib.oracle_pack(_p(words), _p(lens), ctypes.c_int(B), ctypes.c_int(max_len),
-                         ctypes.c_int(block), ctypes.c_int(first_block), ctypes.c_int(max_blocks),
-                         _p(out["cu_seqlens"]), _p(out["ids"]), _p(out["pos"]), _p(out["seq_of"]),
-                         _p(out["last_idx"]), _p(out["blk_off"]), _p(out["block_table"]), _p(out["slot"]))
-    if rc != 0:
-        raise ValueError("oracle_pack: empty game or block table too small")
+    out["status"] = lib.oracle_pack(
+        _p(words), _p(lens), ctypes.c_int(B), ctypes.c_int(max_len), ctypes.c_int(block),
+        ctypes.c_int(first_block), ctypes.c_int(max_blocks), ctypes.c_int(pad_id),
+        _p(out["cu_seqlens"]), _p(out["ids"]), _p(out["pos"]), _p(out["seq_of"]),
+        _p(out["last_idx"]), _p(out["blk_off"]), _p(out["block_table"]), _p(out["slot"]))
     return out

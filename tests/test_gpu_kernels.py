@@ -33,7 +33,8 @@ def rb(x):
     return x.to(torch.bfloat16).to(torch.float32)
 
 
-def dev_pack(words, lens, max_len=512, block=16, first_block=0, max_blocks=None, capacity=None):
+def dev_pack(words, lens, max_len=512, block=16, first_block=0, max_blocks=None, capacity=None,
+             pad_id=1996):
     dev = torch.device("cuda:0")
     B = len(lens)
     n = np.minimum(lens, max_len)
@@ -54,7 +55,7 @@ def dev_pack(words, lens, max_len=512, block=16, first_block=0, max_blocks=None,
                              capi.ptr(out["cu_seqlens"]), capi.ptr(in_off), capi.ptr(out["ids"]),
                              capi.ptr(out["pos"]), capi.ptr(out["seq_of"]), capi.ptr(out["last_idx"]),
                              capi.ptr(out["blk_off"]), capi.ptr(out["block_table"]), capi.ptr(out["slot"]),
-                             capi.ptr(out["status"]), capi.stream_ptr())
+                             pad_id, capi.ptr(out["status"]), capi.stream_ptr())
     capi.check(rc, "pack")
     torch.cuda.synchronize()
     res = {k: v.cpu().numpy() for k, v in out.items()}
@@ -86,10 +87,10 @@ def test_pack_bit_exact(case):
         lens = np.ones(1500, np.int32)
     else:
         lens = rng.integers(1, 80, 3000).astype(np.int32)
-    words = random_words(rng, lens)
+    words = random_words(rng, lens)  # ids over the whole vocab: PAD occurs in the larger cases
     got = dev_pack(words, lens, first_block=3)
     ref = opack.pack(words, lens, first_block=3)
-    assert got["status"][0] == 0
+    assert got["status"][0] == ref["status"]
     for k in ("cu_seqlens", "ids", "pos", "seq_of", "last_idx", "blk_off", "block_table", "slot"):
         np.testing.assert_array_equal(got[k], ref[k], err_msg=k)
 
@@ -107,6 +108,12 @@ def test_pack_status_flags():
     assert (got["ids"][:40] == (words[:40] & 0x3FFF)).all()
     got = dev_pack(words, lens, max_blocks=2)  # 40 tokens need 3 blocks of 16
     assert got["status"][0] & 4
+    words = (np.arange(30, dtype=np.uint32) % 1990) | (1 << 16)
+    lens = np.array([10, 20], np.int32)
+    assert dev_pack(words, lens)["status"][0] == 0
+    words[25] = 1996 | (3 << 16)  # a PAD id inside the second game
+    assert dev_pack(words, lens)["status"][0] == 8
+    assert dev_pack(words, lens, pad_id=-1)["status"][0] == 0
 
 
 def _gemm(A, Wt, bias, epi, wtype, out_f32=False, R=None, scale=None):
