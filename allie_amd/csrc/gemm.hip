@@ -6,17 +6,36 @@
 // ``addmm(b, x, W[in,out])`` of GPT-2 [lib transformers Conv1D] with the
 // weights repacked once to [out][in] at load time.
 //
-// MFMA kernel: 256 threads (4 waves, 2 x 2), block tile 256 (M) x 256 (N),
-// BK = 64, double-buffered LDS (2 x 64 KiB) filled by direct global->LDS
-// 16-byte loads (fp8 weights go through registers to be widened to bf16),
-// one block per CU.
-// Each wave owns a 128 x 128 sub-tile = 4 x 4 MFMA 32x32x16 bf16 blocks
-// (256 fp32 accumulators).  The MFMA's first operand is the weight fragment
-// and its second the activation fragment, so each lane's accumulator holds 4
-// consecutive output columns of one row: the epilogue stores 8 (bf16) or 16
-// (fp32) contiguous bytes per lane.  LDS rows are 128 B (64 bf16); 16-byte
-// chunk c of row r sits at chunk position c ^ (r & 7) so the fragment reads of
-// 8 consecutive rows hit 8 distinct chunk positions.
+// MFMA kernel: 256 threads (4 waves, 2 (m) x 2 (n)), block tile 256 (m) x 128
+// (n), two blocks per CU.  Each wave owns a 128 (m) x 64 (n) sub-tile = 2 x 4
+// MFMA 32x32x16 bf16 blocks (128 fp32 accumulators), which leaves room for a
+// second block on every SIMD: while one block sits in its epilogue, prologue
+// or a barrier, the other keeps the matrix cores busy.  (Measured on the
+// 53205 x 4096 x 1024 MLP GEMM with one 256 x 256 block per CU: prologue 7K,
+// k-loop 58K and epilogue 25-75K cycles per tile, the epilogues of all CUs
+// falling together and idling the MFMAs.)
+//
+// k-tiles of BK = 32 go through a ring of STAGES LDS buffers filled by direct
+// global->LDS 16-byte loads; the ring is waited with partial vmcnt counts and
+// a fence-free s_barrier (a __syncthreads() fence would drain every
+// outstanding load).
+//
+// The MFMA's first operand is the weight fragment and its second the
+// activation fragment, so each lane's accumulator holds 4 consecutive output
+// columns of one row.
+//
+// k order inside a k-tile: in MFMA step s (0, 1) the lanes of half h = lane/32
+// multiply k = 16 h + 8 s .. +7.  Both operands use this order, so the sum is
+// unchanged, and it lets an fp8 weight row hand a lane both of its steps' k
+// values as one 16-byte chunk.
+//
+// LDS layouts (gfx950 LDS: 64 banks x 4 B, a 16-byte read serves 16 lanes per
+// clock, so 16 consecutive rows must hit 16 distinct 16-byte slots of a
+// 256-byte window):
+//   bf16 rows of 64 B (4 chunks):  chunk c of row r at c ^ ((r >> 2) & 3)
+//   fp8  rows of 32 B (2 chunks):  chunk c of row r at c ^ ((r >> 3) & 1)
+// Fragment reads are double-buffered in registers: the reads of step s + 1 are
+// issued while the MFMAs of step s run.
 //
 // Block order: workgroups are dealt round-robin to the 8 XCDs, so block id
 // pid runs on XCD pid % 8; tiles are renumbered so that each XCD walks a
@@ -27,7 +46,9 @@
 //   EPI_STORE  C = bf16(acc + b)               (QKV projection)
 //   EPI_GELU   C = bf16(gelu(bf16(acc + b)))   (MLP c_fc + gelu_new)
 //   EPI_RESID  R += bf16(acc + b)              (attn c_proj / MLP c_proj)
-// with fp32 output (no rounding) when out_f32 is set (heads).
+// with fp32 output (no rounding) when out_f32 is set (heads).  fp8 weights:
+// acc is multiplied by the output channel's scale before the bias.  bf16
+// results are transposed through LDS so global memory sees 128-byte rows.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -35,11 +56,20 @@ namespace {
 
 using namespace allie;
 
-constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int BM = 256, BN = 128, BK = 32;
+constexpr int STAGES = 3;
 constexpr int NTHREADS = 256;
+constexpr int FM = 4, FN = 2;     // 32x32 MFMA blocks per wave along m and n
 constexpr int GROUP_M = 4;
+constexpr int A_STAGE = BM * BK;  // bf16 elements per A stage (16 KiB)
+constexpr int W_STAGE = BN * BK;  // bf16 elements per W stage (8 KiB; fp8 uses half)
+constexpr int EP = 72;            // epilogue transpose row pitch (bf16): 64 + 8 pad
+static_assert(4 * 128 * EP <= STAGES * (A_STAGE + W_STAGE), "epilogue region fits the ring");
 
-ALLIE_DEV int swz(int row, int chunk) { return row * BK + ((chunk ^ (row & 7)) << 3); }
+// element offset of logical 16-byte chunk c of row r in a bf16 stage
+ALLIE_DEV int swz16(int r, int c) { return r * BK + ((c ^ ((r >> 2) & 3)) << 3); }
+// byte offset of logical 16-byte chunk c of row r in an fp8 stage
+ALLIE_DEV int swz8(int r, int c) { return r * BK + ((c ^ ((r >> 3) & 1)) << 4); }
 
 ALLIE_DEV void tile_coords(int pid, int G, int num_tm, int num_tn, int& tm, int& tn) {
   // XCD-aware renumbering: XCD x = pid % 8 takes a contiguous logical range
@@ -57,26 +87,6 @@ ALLIE_DEV void tile_coords(int pid, int G, int num_tm, int num_tn, int& tm, int&
   tn = in_group / gm;
 }
 
-// fp8 weight tile (256 rows x 64 e4m3, register staged: 4 x 16 bytes per
-// thread) -> bf16 into the swizzled LDS layout.
-ALLIE_DEV void fp8_tile_to_lds(const uint4* rw, bf16_t* sw, int tid) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = (tid >> 2) + 64 * i;
-    const uint32_t w4[4] = {rw[i].x, rw[i].y, rw[i].z, rw[i].w};
-    uint32_t o[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t v = w4[j];
-      o[2 * j] = fp8e4m3_to_bf16(v & 0xffu) | (fp8e4m3_to_bf16((v >> 8) & 0xffu) << 16);
-      o[2 * j + 1] = fp8e4m3_to_bf16((v >> 16) & 0xffu) | (fp8e4m3_to_bf16(v >> 24) << 16);
-    }
-    const int c = (tid & 3) * 2;
-    *reinterpret_cast<uint4*>(&sw[swz(row, c)]) = make_uint4(o[0], o[1], o[2], o[3]);
-    *reinterpret_cast<uint4*>(&sw[swz(row, c + 1)]) = make_uint4(o[4], o[5], o[6], o[7]);
-  }
-}
-
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Direct global -> LDS copy of 16 bytes per lane: the wave writes 1 KiB of
@@ -84,12 +94,59 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 ALLIE_DEV void g2l_16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (lds_void_t*)lds, 16, 0, 0);
 }
-ALLIE_DEV void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Wait until at most n_tiles k-tiles' worth (VMT instructions each) of this
+// wave's vector-memory operations are pending; the oldest complete first.
+template <int VMT>
+ALLIE_DEV void wait_vm_tiles(int n_tiles) {
+  switch (n_tiles) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(VMT) : "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * VMT) : "memory"); break;
+  }
+}
+static_assert(STAGES - 1 <= 2, "wait_vm_tiles covers up to two newer tiles in flight");
+
+// Workgroup barrier without a memory fence: LDS reads issued before it have
+// completed (lgkmcnt(0)); the compiler may not move memory accesses across it.
+ALLIE_DEV void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Scheduling hint for one k-step (the next step's NR fragment reads and this
+// step's NM MFMAs): one LDS read after each early MFMA, so the reads are
+// issued early and the remaining MFMAs cover their latency.
+template <int NR, int NM>
+ALLIE_DEV void interleave_step() {
+  static_assert(NR <= NM, "one read per MFMA at most");
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+  }
+  if (NM > NR) __builtin_amdgcn_sched_group_barrier(0x008, NM - NR, 0);
+}
+
+// 8 fp8 e4m3 (two dwords) -> 8 bf16 packed in 4 dwords (exact).
+ALLIE_DEV u32x4_t fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
+  u32x4_t o;
+  o.x = fp8e4m3_to_bf16(lo & 0xffu) | (fp8e4m3_to_bf16((lo >> 8) & 0xffu) << 16);
+  o.y = fp8e4m3_to_bf16((lo >> 16) & 0xffu) | (fp8e4m3_to_bf16(lo >> 24) << 16);
+  o.z = fp8e4m3_to_bf16(hi & 0xffu) | (fp8e4m3_to_bf16((hi >> 8) & 0xffu) << 16);
+  o.w = fp8e4m3_to_bf16((hi >> 16) & 0xffu) | (fp8e4m3_to_bf16(hi >> 24) << 16);
+  return o;
+}
 
 template <int EPI, int WT, bool OUT_F32>
-__global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(1024))) bf16_t sA[2][BM * BK];
-  __shared__ __attribute__((aligned(1024))) bf16_t sW[2][BN * BK];
+__global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
+  // one LDS arena: the ring of A stages, the ring of W stages; the epilogue
+  // reuses it to transpose the output tile
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[STAGES * (A_STAGE + W_STAGE)];
+  auto sA = [&](int s) { return smem + s * A_STAGE; };
+  auto sW = [&](int s) { return smem + STAGES * A_STAGE + s * W_STAGE; };
+  constexpr bool FP8 = WT == W_FP8;
+  // vector-memory instructions per wave per k-tile: A 4, W 2 (bf16) or 1 (fp8)
+  constexpr int VMT = FP8 ? 5 : 6;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (LDS-DMA base)
@@ -98,141 +155,227 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs a) {
   tile_coords(blockIdx.x, gridDim.x, num_tm, num_tn, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int K = a.K;
-  const bf16_t* __restrict__ A = reinterpret_cast<const bf16_t*>(a.A);
-
-  // Loader geometry: wave w fills rows [64 w, 64 w + 64) of each tile with 8
-  // LDS-DMA instructions of 8 rows; lane -> (row 8 i + lane / 8, physical
-  // chunk lane % 8), reading logical chunk (lane % 8) ^ (row & 7).
-  const int lr = lane >> 3, pc = lane & 7, lcg = pc ^ lr;
-  // rows of this lane: m0 + 64 wave + 8 i + lr (i = 0..7); rows at or past M
-  // read the last valid row instead (their results are discarded)
-  const int m_first = m0 + wave * 64 + lr;
-  const int m_last_ok = a.M - 1 - m_first;  // copy i is in range iff 8 i <= m_last_ok
-  const bf16_t* a_row0 = A + (int64_t)(m_first < a.M ? m_first : a.M - 1) * a.lda + lcg * 8;
-  const bf16_t* a_last = A + (int64_t)(a.M - 1) * a.lda + lcg * 8;
-  const int64_t a_step = (int64_t)8 * a.lda;
-  const bf16_t* __restrict__ Wb = reinterpret_cast<const bf16_t*>(a.W);
-  const bf16_t* w_row0 = Wb + (int64_t)(n0 + wave * 64 + lr) * K + lcg * 8;
-  const int64_t w_step = (int64_t)8 * K;
-  const uint8_t* __restrict__ W8 = reinterpret_cast<const uint8_t*>(a.W);
-  uint4 rw[4];
-
-  f32x16_t acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
-
-  const int wm = wave & 1, wn = wave >> 1;
-  const int frow = lane & 31, fgrp = lane >> 5;
   const int KT = K / BK;
 
-#define ISSUE_A(buf, k0)                                                              \
-  _Pragma("unroll") for (int i = 0; i < 8; ++i) {                                     \
-    const bf16_t* src = (8 * i <= m_last_ok) ? a_row0 + (int64_t)i * a_step : a_last; \
-    g2l_16(src + (k0), &sA[buf][(wave * 64 + 8 * i) * BK]);                           \
-  }
-#define ISSUE_W(buf, k0)                                                              \
-  _Pragma("unroll") for (int i = 0; i < 8; ++i)                                       \
-    g2l_16(w_row0 + (int64_t)i * w_step + (k0), &sW[buf][(wave * 64 + 8 * i) * BK]);
-
-  // ---- prologue: stage tile 0 ---------------------------------------------
-  ISSUE_A(0, 0);
-  if constexpr (WT == W_FP8) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = (tid >> 2) + 64 * i;
-      rw[i] = *reinterpret_cast<const uint4*>(W8 + (int64_t)(n0 + row) * K + (tid & 3) * 16);
-    }
-  } else {
-    ISSUE_W(0, 0);
-  }
-  if constexpr (WT == W_FP8) fp8_tile_to_lds(rw, &sW[0][0], tid);
-  wait_vmem();
-  __syncthreads();
-
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    const bool more = kt + 1 < KT;
-    if (more) {
-      const int k1 = (kt + 1) * BK;
-      ISSUE_A(buf ^ 1, k1);
-      if constexpr (WT == W_FP8) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int row = (tid >> 2) + 64 * i;
-          rw[i] = *reinterpret_cast<const uint4*>(W8 + (int64_t)(n0 + row) * K + k1 + (tid & 3) * 16);
-        }
-      } else {
-        ISSUE_W(buf ^ 1, k1);
-      }
-    }
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      const int c = kk * 2 + fgrp;
-      bf16x8_t wf[4], xf[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int rn = wn * 128 + i * 32 + frow;
-        wf[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(&sW[buf][swz(rn, c)]));
-        const int rm = wm * 128 + i * 32 + frow;
-        xf[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(&sA[buf][swz(rm, c)]));
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], xf[j], acc[i][j], 0, 0, 0);
-    }
-    if constexpr (WT == W_FP8) {
-      if (more) fp8_tile_to_lds(rw, &sW[buf ^ 1][0], tid);
-    }
-    wait_vmem();
-    __syncthreads();
-  }
-#undef ISSUE_A
-#undef ISSUE_W
-
-  // ---- epilogue ------------------------------------------------------------
+  // ---- loader geometry ----------------------------------------------------
+  // bf16 rows of 64 B, 16 rows per DMA instruction: lane -> row lane / 4,
+  // physical chunk lane % 4, which holds logical chunk (lane % 4) ^ ((row >> 2) & 3).
+  // A: wave w fills rows [64 w, 64 w + 64) (4 instructions); W: rows
+  // [32 w, 32 w + 32) (2 instructions).
+  const int lr16 = lane >> 2;
+  const int lc16 = (lane & 3) ^ ((lr16 >> 2) & 3);
+  const bf16_t* __restrict__ A = reinterpret_cast<const bf16_t*>(a.A);
+  // rows at or past M read the last valid row instead (results discarded)
+  const bf16_t* a_src[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
+    int m = m0 + wave * 64 + 16 * i + lr16;
+    m = m < a.M ? m : a.M - 1;
+    a_src[i] = A + (int64_t)m * a.lda + lc16 * 8;
+  }
+  const bf16_t* __restrict__ Wb = reinterpret_cast<const bf16_t*>(a.W);
+  const bf16_t* w_src = Wb + (int64_t)(n0 + wave * 32 + lr16) * K + lc16 * 8;
+  const int64_t w_step16 = (int64_t)16 * K;
+  // fp8 rows of 32 B, 32 rows per DMA instruction: lane -> row lane / 2,
+  // physical chunk lane % 2; wave w fills rows [32 w, 32 w + 32).
+  const int lr8 = lane >> 1;
+  const int lc8 = (lane & 1) ^ ((lr8 >> 3) & 1);
+  const uint8_t* __restrict__ W8 = reinterpret_cast<const uint8_t*>(a.W);
+  const uint8_t* w8_src = W8 + (int64_t)(n0 + wave * 32 + lr8) * K + lc8 * 16;
+
+  auto issue = [&](int kt, int s) {
+    const int k0 = kt * BK;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int n = n0 + wn * 128 + i * 32 + q * 8 + fgrp * 4;
-      float4 bias = a.bias ? *reinterpret_cast<const float4*>(a.bias + n) : make_float4(0, 0, 0, 0);
-      float4 scl = make_float4(1, 1, 1, 1);
-      if constexpr (WT == W_FP8) scl = *reinterpret_cast<const float4*>(a.scale + n);
+    for (int i = 0; i < 4; ++i) g2l_16(a_src[i] + k0, sA(s) + (wave * 64 + 16 * i) * BK);
+    if constexpr (FP8) {
+      g2l_16(w8_src + k0, reinterpret_cast<uint8_t*>(sW(s)) + wave * 32 * BK);
+    } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int m = m0 + wm * 128 + j * 32 + frow;
-        if (m >= a.M) continue;
-        float v0 = acc[i][j][q * 4 + 0] * scl.x + bias.x;
-        float v1 = acc[i][j][q * 4 + 1] * scl.y + bias.y;
-        float v2 = acc[i][j][q * 4 + 2] * scl.z + bias.z;
-        float v3 = acc[i][j][q * 4 + 3] * scl.w + bias.w;
-        if constexpr (EPI == EPI_GELU) {
-          v0 = gelu_tanh_fast(round_bf16(v0));
-          v1 = gelu_tanh_fast(round_bf16(v1));
-          v2 = gelu_tanh_fast(round_bf16(v2));
-          v3 = gelu_tanh_fast(round_bf16(v3));
-        }
-        if constexpr (EPI == EPI_RESID) {
-          float4* r = reinterpret_cast<float4*>(a.R + (int64_t)m * a.ldr + n);
-          float4 h = *r;
-          h.x += round_bf16(v0);
-          h.y += round_bf16(v1);
-          h.z += round_bf16(v2);
-          h.w += round_bf16(v3);
-          *r = h;
-        } else if constexpr (OUT_F32) {
+      for (int i = 0; i < 2; ++i) g2l_16(w_src + i * w_step16 + k0, sW(s) + (wave * 32 + 16 * i) * BK);
+    }
+  };
+
+  f32x16_t acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acc[i][j] = f32x16_t{};
+
+  const int wm = wave & 1, wn = wave >> 1;
+  const int frow = lane & 31, half = lane >> 5;
+
+  // fragments of step `st` of the k-tile in stage s
+  auto load_a = [&](int s, int st, bf16x8_t(&xf)[FM]) {
+    const int c = 2 * half + st;
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const int r = wm * 128 + j * 32 + frow;
+      xf[j] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(sA(s) + swz16(r, c)));
+    }
+  };
+  auto load_w = [&](int s, int st, bf16x8_t(&wf)[FN]) {
+    const int c = 2 * half + st;
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+      const int r = wn * 64 + i * 32 + frow;
+      wf[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(sW(s) + swz16(r, c)));
+    }
+  };
+  // fp8: one 16-byte read per weight fragment row holds both steps
+  auto load_w8 = [&](int s, u32x4_t(&wq)[FN]) {
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(sW(s));
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+      const int r = wn * 64 + i * 32 + frow;
+      wq[i] = *reinterpret_cast<const u32x4_t*>(base + swz8(r, half));
+    }
+  };
+  auto widen_w8 = [&](const u32x4_t(&wq)[FN], int st, bf16x8_t(&wf)[FN]) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+      wf[i] = __builtin_bit_cast(bf16x8_t, st == 0 ? fp8x8_to_bf16x8(wq[i].x, wq[i].y)
+                                                   : fp8x8_to_bf16x8(wq[i].z, wq[i].w));
+  };
+  auto mfma_step = [&](const bf16x8_t(&wf)[FN], const bf16x8_t(&xf)[FM]) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], xf[j], acc[i][j], 0, 0, 0);
+  };
+  constexpr int NMF = FN * FM;  // MFMAs per step
+
+  // ---- prologue: fill the ring (tile 0 must land) ---------------------------
+  const int n_pre = KT < STAGES ? KT : STAGES;
+  for (int t = 0; t < n_pre; ++t) issue(t, t);
+  wait_vm_tiles<VMT>(n_pre - 1);
+  lds_barrier();
+
+  bf16x8_t wP[FN], xP[FM], wQ[FN], xQ[FM];
+  u32x4_t w8[FN];
+  if constexpr (FP8) {
+    load_w8(0, w8);
+    load_a(0, 0, xP);
+    widen_w8(w8, 0, wP);
+  } else {
+    load_w(0, 0, wP);
+    load_a(0, 0, xP);
+  }
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const int s = kt % STAGES;
+    const int s1 = (kt + 1) % STAGES;
+    // step 0: read step 1's fragments, multiply step 0's
+    if constexpr (FP8) {
+      widen_w8(w8, 1, wQ);
+      load_a(s, 1, xQ);
+      mfma_step(wP, xP);
+      interleave_step<FM, NMF>();
+    } else {
+      load_w(s, 1, wQ);
+      load_a(s, 1, xQ);
+      mfma_step(wP, xP);
+      interleave_step<FN + FM, NMF>();
+    }
+    // step 1: tile kt + 1 must have landed; then recycle stage s for tile
+    // kt + STAGES and read the next tile's first fragments
+    {
+      int newer = KT - kt - 2;
+      newer = newer < STAGES - 2 ? newer : STAGES - 2;
+      wait_vm_tiles<VMT>(newer > 0 ? newer : 0);
+    }
+    lds_barrier();
+    if (kt + STAGES < KT) issue(kt + STAGES, s);
+    // after the last tile these read a stale (in-bounds) stage, never used
+    if constexpr (FP8) {
+      load_w8(s1, w8);
+      load_a(s1, 0, xP);
+      mfma_step(wQ, xQ);
+      interleave_step<FN + FM, NMF>();
+      widen_w8(w8, 0, wP);
+    } else {
+      load_w(s1, 0, wP);
+      load_a(s1, 0, xP);
+      mfma_step(wQ, xQ);
+      interleave_step<FN + FM, NMF>();
+    }
+  }
+
+  // ---- epilogue ------------------------------------------------------------
+  // accumulator element (i, j, q, e) is output (m, n) with
+  // m = m0 + wm 128 + j 32 + frow, n = n0 + wn 64 + i 32 + q 8 + half 4 + e
+  auto epi_value = [&](float v, float scl, float bias) {
+    v = v * scl + bias;
+    if constexpr (EPI == EPI_GELU) v = gelu_tanh_fast(round_bf16(v));
+    return v;
+  };
+  const int n_base = n0 + wn * 64;
+  if constexpr (OUT_F32) {
+    // heads (small M): direct 16-byte stores of fp32 rows
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n_base + i * 32 + q * 8 + half * 4;
+        const float4 bias = a.bias ? *reinterpret_cast<const float4*>(a.bias + n) : make_float4(0, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+          const int m = m0 + wm * 128 + j * 32 + frow;
+          if (m >= a.M) continue;
           *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.C) + (int64_t)m * a.ldc + n) =
-              make_float4(v0, v1, v2, v3);
-        } else {
-          uint2 p;
-          p.x = pack_bf16x2(v0, v1);
-          p.y = pack_bf16x2(v2, v3);
-          *reinterpret_cast<uint2*>(reinterpret_cast<bf16_t*>(a.C) + (int64_t)m * a.ldc + n) = p;
+              make_float4(epi_value(acc[i][j][q * 4 + 0], 1.f, bias.x), epi_value(acc[i][j][q * 4 + 1], 1.f, bias.y),
+                          epi_value(acc[i][j][q * 4 + 2], 1.f, bias.z), epi_value(acc[i][j][q * 4 + 3], 1.f, bias.w));
         }
+      }
+    }
+  } else {
+    // bf16 results go through LDS so that global memory sees whole 128-byte
+    // row segments: each wave writes its 128 (m) x 64 (n) sub-tile into a
+    // private region of rows padded to EP bf16, then reads it back 16 bytes
+    // per lane, 8 lanes per row.
+    lds_barrier();  // every wave is done with the ring
+    bf16_t* reg = smem + wave * 128 * EP;
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int nl = i * 32 + q * 8 + half * 4;  // column inside the sub-tile
+        const float4 bias = a.bias ? *reinterpret_cast<const float4*>(a.bias + n_base + nl)
+                                   : make_float4(0, 0, 0, 0);
+        float4 scl = make_float4(1, 1, 1, 1);
+        if constexpr (FP8) scl = *reinterpret_cast<const float4*>(a.scale + n_base + nl);
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+          const int ml = j * 32 + frow;
+          uint2 p;
+          p.x = pack_bf16x2(epi_value(acc[i][j][q * 4 + 0], scl.x, bias.x),
+                            epi_value(acc[i][j][q * 4 + 1], scl.y, bias.y));
+          p.y = pack_bf16x2(epi_value(acc[i][j][q * 4 + 2], scl.z, bias.z),
+                            epi_value(acc[i][j][q * 4 + 3], scl.w, bias.w));
+          *reinterpret_cast<uint2*>(reg + ml * EP + nl) = p;
+        }
+      }
+    }
+    // read back: lane -> row (lane / 8) + 8 it, columns 8 (lane % 8) .. +7
+    const int cl = (lane & 7) * 8;
+#pragma unroll 4
+    for (int it = 0; it < 16; ++it) {
+      const int ml = it * 8 + (lane >> 3);
+      const int m = m0 + wm * 128 + ml;
+      const uint4 v = *reinterpret_cast<const uint4*>(reg + ml * EP + cl);
+      if (m >= a.M) continue;
+      if constexpr (EPI == EPI_RESID) {
+        // R += the bf16-rounded value (exact in fp32)
+        float4* r = reinterpret_cast<float4*>(a.R + (int64_t)m * a.ldr + n_base + cl);
+        float4 h0 = r[0], h1 = r[1];
+        h0.x += bf2f(v.x & 0xffffu); h0.y += bf2f(v.x >> 16);
+        h0.z += bf2f(v.y & 0xffffu); h0.w += bf2f(v.y >> 16);
+        h1.x += bf2f(v.z & 0xffffu); h1.y += bf2f(v.z >> 16);
+        h1.z += bf2f(v.w & 0xffffu); h1.w += bf2f(v.w >> 16);
+        r[0] = h0;
+        r[1] = h1;
+      } else {
+        *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(a.C) + (int64_t)m * a.ldc + n_base + cl) = v;
       }
     }
   }
