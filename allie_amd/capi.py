@@ -53,7 +53,7 @@ _SIGS = [
     ("allie_pack_ragged", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
       C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
-      C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]),
+      C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]),
     ("allie_prefill_workspace_bytes", C.c_size_t, [C.c_void_p, C.c_int, C.c_int]),
     ("allie_kv_block_bytes", C.c_size_t, [C.c_void_p]),
     ("allie_prefill", C.c_int,

@@ -90,6 +90,35 @@ def cpu_baseline(cfg, sd, seqs, budget_s: float = 20.0):
     }
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gemm_fc_c2.txt")
+
+
+def read_traffic():
+    """HBM bytes per launch of the fc GEMM, measured with rocprofv3 --pmc
+    FETCH_SIZE / WRITE_SIZE and scaled by the copy calibration (the line
+    ``hbm_bytes_per_launch: N`` of the committed summary), or None."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    with open(TRAFFIC_FILE) as f:
+        for line in f:
+            if line.startswith("hbm_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    return None
+
+
+def calibrate_copy(mib: int = 512, reps: int = 3):
+    """A plain device-to-device copy of known size, for scaling the HBM byte
+    counters (FETCH_SIZE / WRITE_SIZE) of the profiled kernels."""
+    import torch
+
+    x = torch.empty(mib * 1024 * 1024, dtype=torch.uint8, device="cuda:0").fill_(1)
+    y = torch.empty_like(x)
+    for _ in range(reps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration_copy_bytes": x.numel(), "reps": reps}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -97,11 +126,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 512 MiB device copy (counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(the path shards by game with no exchange; see DESIGN.md)"}))
         sys.exit(2)
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
 
     import torch
 
@@ -135,11 +169,7 @@ def main():
     fc_flops = 2.0 * T * cfg.d_ff * cfg.d_model
     fc_ms = tot_ms.value / max(n_l.value, 1)
     fc_tflops = fc_flops / (fc_ms * 1e-3) / 1e12
-    traffic = None
-    tp = os.path.join(ROOT, "profiles", "gemm_fc_c2_traffic.json")
-    if os.path.exists(tp):
-        with open(tp) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    traffic = read_traffic()
     res = {
         "metric": "leaf evals/sec @ medium, ragged batch 256; % of MFMA / HBM roofline",
         "value": 256.0 / (ms / 1000.0),

@@ -13,13 +13,28 @@ from allie_amd import capi
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def declared_functions():
-    names = []
+def declared_signatures():
+    """name -> number of parameters, for every function in include/*.h."""
+    sigs = {}
     for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
         src = open(h).read()
         src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-        names += re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(allie_[a-z_0-9]+)\s*\(", src, flags=re.M)
-    return sorted(set(names))
+        for m in re.finditer(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(allie_[a-z_0-9]+)\s*\(([^)]*)\)\s*;",
+                             src, flags=re.M):
+            params = " ".join(m.group(2).split())
+            sigs[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return sigs
+
+
+def declared_functions():
+    return sorted(declared_signatures())
+
+
+def test_ctypes_signatures_match_header():
+    sigs = declared_signatures()
+    for name, res, args in capi._SIGS:
+        assert name in sigs, name
+        assert len(args) == sigs[name], (name, len(args), sigs[name])
 
 
 def test_library_exports_every_declared_symbol():
