@@ -58,8 +58,16 @@ _SIGS = [
     ("allie_kv_block_bytes", C.c_size_t, [C.c_void_p]),
     ("allie_prefill", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_float, C.c_void_p, C.c_int,
-      C.POINTER(AllieOutputs), C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_size_t,
-      C.c_void_p]),
+      C.POINTER(AllieOutputs), C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int,
+      C.c_void_p, C.c_size_t, C.c_void_p]),
+    ("allie_extend_workspace_bytes", C.c_size_t, [C.c_void_p, C.c_int, C.c_int]),
+    ("allie_extend", C.c_int,
+     [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,            # model, ids, pos, n_tok
+      C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int,   # groups, prefix_len/blocks, max_blocks
+      C.c_void_p, C.c_void_p, C.c_int,                        # extra_slot, n_extra, max_extra
+      C.c_float, C.c_void_p, C.c_int, C.POINTER(AllieOutputs),  # temperature, legal, words, out
+      C.c_void_p, C.c_int, C.c_void_p,                        # kv_pool, pool blocks, status
+      C.c_void_p, C.c_size_t, C.c_void_p]),                   # workspace, bytes, stream
     ("allie_probe_begin", C.c_int, [C.c_int, C.c_int]),
     ("allie_probe_end", C.c_int, [C.POINTER(C.c_float), C.POINTER(C.c_int)]),
     ("allie_gemm", C.c_int,

@@ -13,8 +13,11 @@
 // likewise accumulated transposed, O^T = V^T P^T: P^T is already in the
 // B-operand layout lane by lane (after a fixed permutation of the key index
 // that is applied identically to V^T), and V^T comes from a transposed,
-// padded LDS copy of the value tile.  Online softmax in fp32 with exp2; P is
-// rounded to bf16 for the PV product.
+// padded LDS copy of the value tile.  Online softmax in fp32 with exp2; P
+// enters the PV product as two bf16 MFMA operands, hi = bf16(p) and
+// lo = bf16(p - hi), so the weights keep ~16 mantissa bits (a single bf16 P
+// costs up to 2^-9 relative per weight, enough to flip the bf16 rounding of
+// many attention outputs against an fp32-softmax reference).
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -131,10 +134,10 @@ __global__ __launch_bounds__(128) void attn_varlen_bf16_kernel(AttnVarlenArgs a)
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) {
-        uint32_t pw[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) pw[e] = pack_bf16x2(st[b][mm * 8 + 2 * e], st[b][mm * 8 + 2 * e + 1]);
-        bf16x8_t pf = __builtin_bit_cast(bf16x8_t, u32x4_t{pw[0], pw[1], pw[2], pw[3]});
+        // P = P_hi + P_lo, both bf16: the PV product keeps ~16 mantissa bits of
+        // the fp32 probabilities instead of bf16's 8
+        bf16x8_t pf, pl;
+        if (mm == 0) split_bf16x8<0>(st[b], pf, pl); else split_bf16x8<8>(st[b], pf, pl);
         const int kb = b * 32 + mm * 16 + 4 * g;  // keys kb..kb+3 and kb+8..kb+11
 #pragma unroll
         for (int hb = 0; hb < 2; ++hb) {
@@ -143,6 +146,7 @@ __global__ __launch_bounds__(128) void attn_varlen_bf16_kernel(AttnVarlenArgs a)
           u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + kb + 8);
           bf16x8_t vf = __builtin_bit_cast(bf16x8_t, u32x4_t{lo.x, lo.y, hi.x, hi.y});
           o[hb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[hb], 0, 0, 0);
+          o[hb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pl, o[hb], 0, 0, 0);
         }
       }
   }
@@ -223,6 +227,7 @@ __global__ __launch_bounds__(256) void kv_write_kernel(KVWriteArgs a) {
   const int per_chunk = 16 / esz;                // elements per 16-byte chunk
   const int chunks = 2 * d / per_chunk;          // k and v of all heads
   const int sl = a.slot[t];
+  if (sl < 0 || (sl >> 4) >= a.pool_blocks) return;  // flagged by the caller's validation
   const int64_t blk = sl >> 4, off = sl & 15;
   const char* src = reinterpret_cast<const char*>(a.qkv) + (t * 3 * d + d) * esz;  // k | v
   for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
@@ -243,6 +248,7 @@ hipError_t launch_attn_varlen(const AttnVarlenArgs& a, hipStream_t st) {
   if (a.head_dim != HD) return hipErrorInvalidValue;
   if (a.act_bf16) {
     if (a.n_tiles == 0) return hipSuccess;
+    if (a.n_tiles > 65535) return hipErrorInvalidValue;  // grid y limit
     hipLaunchKernelGGL(attn_varlen_bf16_kernel, dim3(a.n_head, a.n_tiles), dim3(128), 0, st, a);
   } else {
     if (a.T == 0) return hipSuccess;

@@ -1,0 +1,448 @@
+// Attention of new tokens over a paged KV cache: MCTS tree expansion and
+// continuous-batching decode.
+//
+// The reference has no KV cache: every MCTS leaf and every appended move is a
+// full recompute of the game prefix at batch 1 (src/evaluation/decode.py:
+// 356-360, README.md:80).  What such a recompute yields at the new token is
+// softmax(q K^T / 8) V over all earlier tokens of the same game plus the token
+// itself, which is what these kernels compute from cached keys and values:
+//
+//   keys of token i = its group's shared prefix (a root's game, or a decode
+//                     slot's context), read through the group's block table,
+//                     then the token's private keys (a search node's
+//                     ancestors and the node itself), read slot by slot.
+//
+// Pool layout (one block = 16 positions of every layer):
+//   [block][layer][k|v][head][16][64]  (bf16, or fp32 in the fp32 check mode)
+// so one (block, layer, k|v, head) is a contiguous 2 KiB (bf16) row group.
+//
+// attn_extend_wave_kernel  -- one wave per (token, head); lane l owns key
+//   l / 4 of a 16-key block and head dims 16 (l % 4) .. +15.  Streams the keys
+//   once per query: the decode kernel (groups of one token).
+// attn_extend_tree_kernel  -- a workgroup per (64-query tile of a group,
+//   head): the group's prefix keys are staged through LDS once per tile and
+//   multiplied on the MFMA units (S^T = K Q^T, O^T = V^T P^T, as in the
+//   varlen prefill kernel); each query's private keys follow in registers.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace {
+
+using namespace allie;
+
+constexpr int HD = 64;
+constexpr int QT = 64;           // queries per tree-kernel tile
+constexpr int KT = 64;           // prefix keys per LDS tile (4 pool blocks)
+constexpr int VT_LD = KT + 4;    // padded row of the transposed value tile
+constexpr int PREP_THREADS = 1024;
+
+// element offset of (block, layer, k|v, head, offset-in-block, dim 0)
+ALLIE_DEV int64_t pool_off(int64_t blk, int L, int layer, int kv, int H, int head, int off) {
+  return ((((blk * L + layer) * 2 + kv) * H + head) * KV_BLOCK + off) * (int64_t)HD;
+}
+
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(PREP_THREADS) void extend_prepare_kernel(ExtendPrepArgs a) {
+  int bad = 0;
+  for (int i = threadIdx.x; i < a.n; i += PREP_THREADS) {
+    const int ne = a.n_extra[i];
+    int self = -1;
+    if (ne < 1 || ne > a.max_extra) {
+      bad |= 1;
+    } else {
+      for (int e = 0; e < ne; ++e) {
+        const int sl = a.extra_slot[(int64_t)i * a.max_extra + e];
+        if (sl < 0 || (sl >> 4) >= a.pool_blocks) bad |= 2;
+      }
+      self = a.extra_slot[(int64_t)i * a.max_extra + ne - 1];
+    }
+    a.self_slot[i] = self;
+    const int p = a.pos[i];
+    if (p < 0 || p >= a.n_positions) bad |= 4;
+  }
+  for (int g = threadIdx.x; g < a.n_groups; g += PREP_THREADS) {
+    const int P = a.prefix_len[g];
+    const int nb = (P + KV_BLOCK - 1) / KV_BLOCK;
+    if (P < 0 || nb > a.max_blocks) {
+      bad |= 2;
+      continue;
+    }
+    for (int b = 0; b < nb; ++b) {
+      const int blk = a.prefix_blocks[(int64_t)g * a.max_blocks + b];
+      if (blk < 0 || blk >= a.pool_blocks) bad |= 2;
+    }
+  }
+  const int b1 = __syncthreads_or(bad & 1), b2 = __syncthreads_or(bad & 2), b4 = __syncthreads_or(bad & 4);
+  if (threadIdx.x == 0 && a.status) *a.status = (b1 ? 1 : 0) | (b2 ? 2 : 0) | (b4 ? 4 : 0);
+}
+
+// Tile list of the tree kernel: (g << 8) | t for t < ceil(size_g / 64), groups
+// in order.  One workgroup; exclusive scan of the per-group tile counts.
+__global__ __launch_bounds__(PREP_THREADS) void extend_tiles_kernel(const int32_t* __restrict__ group_start,
+                                                                    int G, int32_t* __restrict__ tiles) {
+  __shared__ int sh[PREP_THREADS / 64 + 1];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int carry = 0;
+  for (int base = 0; base < G; base += PREP_THREADS) {
+    const int g = base + threadIdx.x;
+    const int nt = g < G ? (group_start[g + 1] - group_start[g] + QT - 1) / QT : 0;
+    int x = nt;  // inclusive wave scan
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) sh[wave] = x;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int s = 0;
+      for (int w = 0; w < PREP_THREADS / 64; ++w) {
+        const int v = sh[w];
+        sh[w] = s;
+        s += v;
+      }
+      sh[PREP_THREADS / 64] = s;
+    }
+    __syncthreads();
+    const int first = carry + sh[wave] + x - nt;
+    for (int t = 0; t < nt; ++t) tiles[first + t] = (g << 8) | t;
+    carry += sh[PREP_THREADS / 64];
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+template <typename T>
+ALLIE_DEV void load16(const T* p, float (&v)[16]);
+template <>
+ALLIE_DEV void load16<bf16_t>(const bf16_t* p, float (&v)[16]) {
+  const uint4 a = reinterpret_cast<const uint4*>(p)[0], b = reinterpret_cast<const uint4*>(p)[1];
+  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    v[2 * j] = bf2f(w[j] & 0xffffu);
+    v[2 * j + 1] = bf2f(w[j] >> 16);
+  }
+}
+template <>
+ALLIE_DEV void load16<float>(const float* p, float (&v)[16]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float4 f = reinterpret_cast<const float4*>(p)[j];
+    v[4 * j] = f.x;
+    v[4 * j + 1] = f.y;
+    v[4 * j + 2] = f.z;
+    v[4 * j + 3] = f.w;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void attn_extend_wave_kernel(ExtendAttnArgs a) {
+  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int H = a.n_head, d = H * HD;
+  if (wid >= (int64_t)a.n * H) return;  // no barriers below: whole waves leave
+  const int i = (int)(wid / H), head = (int)(wid % H);
+  const int lane = threadIdx.x & 63;
+  const int kj = lane >> 2, dq = (lane & 3) * 16;
+  // group of token i: group_start[g] <= i < group_start[g + 1]
+  int lo = 0, hi = a.n_groups;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (a.group_start[mid] <= i) lo = mid; else hi = mid;
+  }
+  const int g = lo;
+  const T* __restrict__ qkv = reinterpret_cast<const T*>(a.qkv);
+  const T* __restrict__ pool = reinterpret_cast<const T*>(a.pool);
+  const float sl2 = a.scale * 1.4426950408889634f;  // scale * log2(e)
+  float q[16];
+  load16<T>(qkv + (int64_t)i * 3 * d + head * HD + dq, q);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) q[j] *= sl2;
+
+  float m_run = -INFINITY, l_run = 0.f, acc[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.f;
+
+  // one 16-key block: lane's key is (blk, off) if ok
+  auto step = [&](int64_t blk, int off, bool ok) {
+    float kv[16];
+    float s = -INFINITY;
+    if (ok) {
+      load16<T>(pool + pool_off(blk, a.n_layer, a.layer, 0, H, head, off) + dq, kv);
+      s = 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) s = fmaf(q[j], kv[j], s);
+    }
+    s += __shfl_xor(s, 1, 64);  // the 4 lanes of a key share ok, so -inf stays -inf
+    s += __shfl_xor(s, 2, 64);
+    float mb = s;
+#pragma unroll
+    for (int o = 4; o < 64; o <<= 1) mb = fmaxf(mb, __shfl_xor(mb, o, 64));
+    const float m_new = fmaxf(m_run, mb);
+    if (m_new == -INFINITY) return;  // nothing visible yet (wave-uniform)
+    const float alpha = exp2f(m_run - m_new);
+    const float p = ok ? exp2f(s - m_new) : 0.f;
+    l_run = l_run * alpha + ((lane & 3) == 0 ? p : 0.f);
+    if (ok) load16<T>(pool + pool_off(blk, a.n_layer, a.layer, 1, H, head, off) + dq, kv);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = acc[j] * alpha + (ok ? p * kv[j] : 0.f);
+    m_run = m_new;
+  };
+
+  const int P = a.prefix_len[g];
+  const int nb = (P + KV_BLOCK - 1) / KV_BLOCK;
+  for (int b = 0; b < nb && b < a.max_blocks; ++b) {
+    const int blk = a.prefix_blocks[(int64_t)g * a.max_blocks + b];
+    const bool ok = blk >= 0 && blk < a.pool_blocks && b * KV_BLOCK + kj < P;
+    step(ok ? blk : 0, kj, ok);
+  }
+  int E = a.n_extra[i];
+  E = E < 0 ? 0 : (E > a.max_extra ? a.max_extra : E);
+  for (int e0 = 0; e0 < E; e0 += 16) {
+    const int e = e0 + kj;
+    const int sl = e < E ? a.extra_slot[(int64_t)i * a.max_extra + e] : -1;
+    const bool ok = sl >= 0 && (sl >> 4) < a.pool_blocks;
+    step(ok ? (sl >> 4) : 0, sl & 15, ok);
+  }
+  // combine the 16 key lanes of each head-dim group
+#pragma unroll
+  for (int o = 4; o < 64; o <<= 1) {
+    l_run += __shfl_xor(l_run, o, 64);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] += __shfl_xor(acc[j], o, 64);
+  }
+  l_run += __shfl_xor(l_run, 1, 64);
+  l_run += __shfl_xor(l_run, 2, 64);
+  if (kj != 0) return;
+  const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
+  if constexpr (sizeof(T) == 2) {
+    uint32_t w[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w[j] = pack_bf16x2(acc[2 * j] * inv, acc[2 * j + 1] * inv);
+    uint4* o = reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(a.out) + (int64_t)i * d + head * HD + dq);
+    o[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    o[1] = make_uint4(w[4], w[5], w[6], w[7]);
+  } else {
+    float4* o = reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + (int64_t)i * d + head * HD + dq);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = make_float4(acc[4 * j] * inv, acc[4 * j + 1] * inv, acc[4 * j + 2] * inv, acc[4 * j + 3] * inv);
+  }
+}
+
+// ---------------------------------------------------------------------------
+ALLIE_DEV int kswz(int row, int chunk) { return row * HD + ((chunk ^ (row & 7)) << 3); }
+
+__global__ __launch_bounds__(128) void attn_extend_tree_kernel(ExtendAttnArgs a) {
+  __shared__ __attribute__((aligned(16))) bf16_t sK[KT * HD];
+  __shared__ __attribute__((aligned(16))) bf16_t sVt[HD * VT_LD];
+
+  const int head = blockIdx.y;
+  const int tile = a.tiles[blockIdx.x];
+  const int g = tile >> 8, qt = tile & 255;
+  const int H = a.n_head, d = H * HD, ld = 3 * d;
+  const int q_end = a.group_start[g + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hf = lane >> 5, ql = lane & 31;
+  const bf16_t* __restrict__ qkv = reinterpret_cast<const bf16_t*>(a.qkv);
+  const bf16_t* __restrict__ pool = reinterpret_cast<const bf16_t*>(a.pool);
+
+  const int qi = a.group_start[g] + qt * QT + wave * 32 + ql;
+  const bool q_ok = qi < q_end;
+  bf16x8_t qf[4];  // B operand of S^T = K Q^T: head dims 16 kk + 8 hf .. +7
+  {
+    const bf16_t* qrow = qkv + (int64_t)(q_ok ? qi : 0) * ld + head * HD;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      u32x4_t v = q_ok ? *reinterpret_cast<const u32x4_t*>(qrow + kk * 16 + hf * 8) : u32x4_t{0, 0, 0, 0};
+      qf[kk] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  }
+  const float sl2 = a.scale * 1.4426950408889634f;
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x16_t o[2] = {f32x16_t{}, f32x16_t{}};
+
+  // ---- phase 1: the group's prefix, 64 keys (4 pool blocks) per LDS tile ----
+  const int P = a.prefix_len[g];
+  const int32_t* btab = a.prefix_blocks + (int64_t)g * a.max_blocks;
+  for (int k0 = 0; k0 < P; k0 += KT) {
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int cidx = tid + 128 * it;  // 512 chunks: 64 keys x 8 chunks
+      const int key = cidx >> 3, c = cidx & 7;
+      const int p = k0 + key;
+      const int bi = p / KV_BLOCK;
+      const int blk = (p < P && bi < a.max_blocks) ? btab[bi] : -1;
+      const bool ok = blk >= 0 && blk < a.pool_blocks;
+      uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+      if (ok) {
+        const int64_t base = pool_off(blk, a.n_layer, a.layer, 0, H, head, p % KV_BLOCK) + c * 8;
+        kv = *reinterpret_cast<const uint4*>(pool + base);
+        vv = *reinterpret_cast<const uint4*>(pool + base + (int64_t)H * KV_BLOCK * HD);  // k -> v
+      }
+      *reinterpret_cast<uint4*>(&sK[kswz(key, c)]) = kv;
+      const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        sVt[(c * 8 + 2 * j) * VT_LD + key] = (bf16_t)(w[j] & 0xffffu);
+        sVt[(c * 8 + 2 * j + 1) * VT_LD + key] = (bf16_t)(w[j] >> 16);
+      }
+    }
+    __syncthreads();
+    f32x16_t st[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      st[b] = f32x16_t{};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        bf16x8_t kf = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(&sK[kswz(b * 32 + ql, kk * 2 + hf)]));
+        st[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], st[b], 0, 0, 0);
+      }
+    }
+    // keys past the prefix (or in a skipped block) are masked
+    float mx = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int p = k0 + b * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
+        const int bi = p / KV_BLOCK;
+        const int blk = (p < P && bi < a.max_blocks) ? btab[bi] : -1;
+        float v = st[b][r] * sl2;
+        if (blk < 0 || blk >= a.pool_blocks) v = -INFINITY;
+        st[b][r] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    if (m_new != -INFINITY) {  // uniform per query (both lanes of a query agree)
+      const float alpha = exp2f(m_run - m_new);
+      m_run = m_new;
+      float ls = 0.f;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = exp2f(st[b][r] - m_new);
+          st[b][r] = p;
+          ls += p;
+        }
+      l_run = l_run * alpha + ls;
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[hb][r] *= alpha;
+    } else {
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) st[b][r] = 0.f;
+    }
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) {
+        bf16x8_t pf, pl;  // P = P_hi + P_lo (see the varlen prefill kernel)
+        if (mm == 0) split_bf16x8<0>(st[b], pf, pl); else split_bf16x8<8>(st[b], pf, pl);
+        const int kb = b * 32 + mm * 16 + 4 * hf;
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+          const bf16_t* vr = &sVt[(hb * 32 + ql) * VT_LD];
+          u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr + kb);
+          u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + kb + 8);
+          bf16x8_t vf = __builtin_bit_cast(bf16x8_t, u32x4_t{lo.x, lo.y, hi.x, hi.y});
+          o[hb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[hb], 0, 0, 0);
+          o[hb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pl, o[hb], 0, 0, 0);
+        }
+      }
+  }
+  if (!q_ok) return;  // no barriers below
+
+  // ---- phase 2: the query's private keys (ancestors, then itself) -----------
+  // lanes l and l ^ 32 share query qi: each holds half of q (dims 16 kk + 8 hf
+  // + [0, 8)) and half of o (dims 32 hb + 8 q4 + 4 hf + [0, 4)).
+  int E = a.n_extra[qi];
+  E = E < 0 ? 0 : (E > a.max_extra ? a.max_extra : E);
+  for (int e = 0; e < E; ++e) {
+    const int sl = a.extra_slot[(int64_t)qi * a.max_extra + e];
+    if (sl < 0 || (sl >> 4) >= a.pool_blocks) continue;  // same decision in both lanes
+    const int64_t kb = pool_off(sl >> 4, a.n_layer, a.layer, 0, H, head, sl & 15);
+    float s = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4_t kw = *reinterpret_cast<const u32x4_t*>(pool + kb + kk * 16 + hf * 8);
+      const u32x4_t qw = __builtin_bit_cast(u32x4_t, qf[kk]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        s = fmaf(bf2f(qw[t] & 0xffffu), bf2f(kw[t] & 0xffffu), s);
+        s = fmaf(bf2f(qw[t] >> 16), bf2f(kw[t] >> 16), s);
+      }
+    }
+    s = (s + __shfl_xor(s, 32, 64)) * sl2;
+    const float m_new = fmaxf(m_run, s);
+    const float alpha = exp2f(m_run - m_new);
+    const float p = exp2f(s - m_new);
+    l_run = l_run * alpha + (hf == 0 ? p : 0.f);
+    const int64_t vb = kb + (int64_t)H * KV_BLOCK * HD;
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const u32x2_t vw = *reinterpret_cast<const u32x2_t*>(pool + vb + hb * 32 + q4 * 8 + 4 * hf);
+        o[hb][q4 * 4 + 0] = o[hb][q4 * 4 + 0] * alpha + p * bf2f(vw.x & 0xffffu);
+        o[hb][q4 * 4 + 1] = o[hb][q4 * 4 + 1] * alpha + p * bf2f(vw.x >> 16);
+        o[hb][q4 * 4 + 2] = o[hb][q4 * 4 + 2] * alpha + p * bf2f(vw.y & 0xffffu);
+        o[hb][q4 * 4 + 3] = o[hb][q4 * 4 + 3] * alpha + p * bf2f(vw.y >> 16);
+      }
+    m_run = m_new;
+  }
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  bf16_t* out = reinterpret_cast<bf16_t*>(a.out) + (int64_t)qi * d + head * HD;
+#pragma unroll
+  for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int hd = hb * 32 + q4 * 8 + 4 * hf;
+      uint2 p;
+      p.x = pack_bf16x2(o[hb][q4 * 4 + 0] * inv, o[hb][q4 * 4 + 1] * inv);
+      p.y = pack_bf16x2(o[hb][q4 * 4 + 2] * inv, o[hb][q4 * 4 + 3] * inv);
+      *reinterpret_cast<uint2*>(out + hd) = p;
+    }
+}
+
+}  // namespace
+
+namespace allie {
+
+hipError_t launch_extend_prepare(const ExtendPrepArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(extend_prepare_kernel, dim3(1), dim3(PREP_THREADS), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_extend_tiles(const int32_t* group_start, int n_groups, int32_t* tiles, hipStream_t st) {
+  if (n_groups == 0) return hipSuccess;
+  hipLaunchKernelGGL(extend_tiles_kernel, dim3(1), dim3(PREP_THREADS), 0, st, group_start, n_groups, tiles);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_extend_wave(const ExtendAttnArgs& a, hipStream_t st) {
+  const int64_t waves = (int64_t)a.n * a.n_head;
+  if (waves == 0) return hipSuccess;
+  const dim3 grid((unsigned)((waves + 3) / 4));
+  if (a.act_bf16)
+    hipLaunchKernelGGL(attn_extend_wave_kernel<bf16_t>, grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(attn_extend_wave_kernel<float>, grid, dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_extend_tree(const ExtendAttnArgs& a, hipStream_t st) {
+  if (!a.act_bf16 || a.tiles == nullptr) return hipErrorInvalidValue;
+  if (a.n_tiles == 0) return hipSuccess;
+  hipLaunchKernelGGL(attn_extend_tree_kernel, dim3(a.n_tiles, a.n_head), dim3(128), 0, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace allie

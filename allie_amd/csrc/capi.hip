@@ -63,8 +63,22 @@ hipError_t probe_mark(int kind, bool before, hipStream_t st) {
 
 }  // namespace
 
+// Pinned host staging for the small host arrays of a call (lengths, group
+// starts): a copy from pageable memory would synchronise the stream, so the
+// array is copied into one of a ring of pinned buffers and uploaded from
+// there.  An event recorded after each upload guards the buffer's reuse.
+struct PinnedRing {
+  static constexpr int N = 4;
+  int32_t* buf[N] = {};
+  size_t cap[N] = {};
+  hipEvent_t ev[N] = {};
+  bool used[N] = {};
+  int next = 0;
+};
+
 struct allie_model {
   allie_config cfg;
+  PinnedRing pinned;
   int d, H, hd, L, V, NH;  // NH: rows of the heads matrix (vocab + 2, padded)
   int wsz;                 // bytes per block-GEMM weight element
   int hsz;                 // bytes per heads-matrix element
@@ -117,6 +131,29 @@ size_t layout_weights(allie_model* m, char* base) {
     l.s_pr = fp8 ? (float*)take(d * 4) : nullptr;
   }
   return off;
+}
+
+// Uploads n int32 from pageable host memory to dst on stream st without
+// synchronising the stream (see PinnedRing).  Not thread-safe per model.
+int upload_i32(allie_model* m, int32_t* dst, const int32_t* host, size_t n, hipStream_t st) {
+  PinnedRing& r = m->pinned;
+  const int i = r.next;
+  r.next = (r.next + 1) % PinnedRing::N;
+  if (r.used[i]) HIP_TRY(hipEventSynchronize(r.ev[i]));  // its previous upload has been consumed
+  if (r.cap[i] < n) {
+    if (r.buf[i]) HIP_TRY(hipHostFree(r.buf[i]));
+    r.buf[i] = nullptr;
+    r.cap[i] = 0;
+    const size_t cap = n < 4096 ? 4096 : n * 2;
+    HIP_TRY(hipHostMalloc((void**)&r.buf[i], cap * 4, hipHostMallocDefault));
+    r.cap[i] = cap;
+  }
+  if (!r.ev[i]) HIP_TRY(hipEventCreateWithFlags(&r.ev[i], hipEventDisableTiming));
+  memcpy(r.buf[i], host, n * 4);
+  HIP_TRY(hipMemcpyAsync(dst, r.buf[i], n * 4, hipMemcpyHostToDevice, st));
+  HIP_TRY(hipEventRecord(r.ev[i], st));
+  r.used[i] = true;
+  return ALLIE_OK;
 }
 
 int check_ready(const allie_model* m) {
@@ -194,6 +231,154 @@ int gemm(const allie_model* m, const void* A, const void* W, const float* bias, 
   return ALLIE_OK;
 }
 
+// Activations of one forward over T token rows.
+struct Acts {
+  float* h;   // [T][d] residual stream (fp32)
+  void* x;    // [T][d] LayerNorm output
+  void* qkv;  // [T][3d]
+  void* attn; // [T][d]
+  void* ff;   // [T][4d]
+};
+
+// The transformer blocks over T rows whose embeddings (h) and first ln_1 (x)
+// are in place.  kv_slot/kv_pool: every layer's keys and values of row t are
+// written to pool slot kv_slot[t] (before attention runs).  attn(layer) runs
+// the attention of one layer from acts.qkv into acts.attn.
+template <typename AttnFn>
+int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slot, void* kv_pool,
+               int kv_pool_blocks, AttnFn&& attn, hipStream_t st) {
+  const int d = m->d, L = m->L, act = m->act_bf16;
+  LNArgs ln{};
+  ln.h = w.h;
+  ln.rows = ln.rows_out = T;
+  ln.d = d;
+  ln.eps = m->cfg.eps;
+  ln.y = w.x;
+  ln.act_bf16 = act;
+  int rc;
+  for (int li = 0; li < L; ++li) {
+    const LayerW& l = m->layers[li];
+    if ((rc = gemm(m, w.x, l.w_qkv, l.b_qkv, l.s_qkv, w.qkv, nullptr, T, 3 * d, d, EPI_STORE, ALLIE_PROBE_QKV, st))) return rc;
+    if (kv_pool && kv_slot) {
+      KVWriteArgs kw{};
+      kw.qkv = w.qkv;
+      kw.slot = kv_slot;
+      kw.T = T;
+      kw.n_layer = L;
+      kw.layer = li;
+      kw.n_head = m->H;
+      kw.head_dim = m->hd;
+      kw.pool_blocks = kv_pool_blocks;
+      kw.pool = kv_pool;
+      kw.act_bf16 = act;
+      HIP_TRY(launch_kv_write(kw, st));
+    }
+    if ((rc = attn(li))) return rc;
+    if ((rc = gemm(m, w.attn, l.w_o, l.b_o, l.s_o, nullptr, w.h, T, d, d, EPI_RESID, ALLIE_PROBE_PROJ, st))) return rc;
+    ln.g = l.ln2_g;
+    ln.b = l.ln2_b;
+    HIP_TRY(launch_layernorm(ln, st));
+    if ((rc = gemm(m, w.x, l.w_fc, l.b_fc, l.s_fc, w.ff, nullptr, T, 4 * d, d, EPI_GELU, ALLIE_PROBE_FC, st))) return rc;
+    if ((rc = gemm(m, w.ff, l.w_pr, l.b_pr, l.s_pr, nullptr, w.h, T, d, 4 * d, EPI_RESID, ALLIE_PROBE_FC2, st))) return rc;
+    if (li + 1 < L) {
+      ln.g = m->layers[li + 1].ln1_g;
+      ln.b = m->layers[li + 1].ln1_b;
+      HIP_TRY(launch_layernorm(ln, st));
+    }
+  }
+  return ALLIE_OK;
+}
+
+// ln_f, the heads GEMM and the heads kernel over `rows` rows of h (row r is
+// h[row_idx[r]], or h[r] when row_idx is null); hx [rows][d] and z
+// [rows][NH] are scratch.
+int run_heads(const allie_model* m, const float* h, const int32_t* row_idx, int rows, void* hx, float* z,
+              float temperature, const uint32_t* legal, int legal_words, const allie_outputs* out,
+              hipStream_t st) {
+  const int d = m->d, act = m->act_bf16;
+  LNArgs lf{};
+  lf.h = h;
+  lf.row_idx = row_idx;
+  lf.rows = lf.rows_out = rows;
+  lf.d = d;
+  lf.g = m->lnf_g;
+  lf.b = m->lnf_b;
+  lf.eps = m->cfg.eps;
+  lf.y = hx;
+  lf.act_bf16 = act;
+  HIP_TRY(launch_layernorm(lf, st));
+  {
+    GemmArgs g{};
+    g.A = hx;
+    g.W = m->w_head;
+    g.bias = m->b_head;
+    g.C = z;
+    g.M = rows;
+    g.N = m->NH;
+    g.K = d;
+    g.lda = d;
+    g.ldc = m->NH;
+    g.epi = EPI_STORE;
+    g.wtype = act ? W_BF16 : W_F32;
+    g.out_f32 = 1;
+    hipError_t e = launch_gemm(g, st);
+    if (e != hipSuccess) return fail(ALLIE_ERR_HIP, "heads gemm: %s", hipGetErrorString(e));
+  }
+  HeadsArgs ha{};
+  ha.z = z;
+  ha.B = rows;
+  ha.ldz = m->NH;
+  ha.vocab = m->V;
+  ha.n_moves = 1968;
+  ha.value_col = m->V;
+  ha.time_col = m->V + 1;
+  ha.temperature = temperature > 1e-5f ? temperature : 1e-5f;
+  ha.legal = legal;
+  ha.legal_words = legal_words;
+  ha.logits = out->logits;
+  ha.value = out->value;
+  ha.time = out->time;
+  ha.top1 = out->top1;
+  ha.lse = out->lse;
+  ha.max_logit = out->max_logit;
+  ha.emulate_bf16 = act;
+  HIP_TRY(launch_heads(ha, st));
+  return ALLIE_OK;
+}
+
+// Workspace of an extend of n tokens in G groups.
+struct ExtendWS {
+  int32_t *group_start, *tiles, *self_slot, *status;
+  float* h;
+  void *x, *qkv, *attn, *ff, *hx;
+  float* z;
+  size_t total;
+};
+
+ExtendWS layout_extend(const allie_model* m, int n, int G, char* base) {
+  ExtendWS w{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) -> char* {
+    char* p = base ? base + off : nullptr;
+    off += align_up(bytes);
+    return p;
+  };
+  const size_t d = m->d, a = m->act_bf16 ? 2 : 4;
+  w.group_start = (int32_t*)take((size_t)(G + 1) * 4);
+  w.tiles = (int32_t*)take(((size_t)n / 64 + G + 1) * 4);  // >= sum of ceil(size / 64)
+  w.self_slot = (int32_t*)take((size_t)n * 4);
+  w.status = (int32_t*)take(4);
+  w.h = (float*)take((size_t)n * d * 4);
+  w.x = take((size_t)n * d * a);
+  w.qkv = take((size_t)n * 3 * d * a);
+  w.attn = take((size_t)n * d * a);
+  w.ff = take((size_t)n * 4 * d * a);
+  w.hx = take((size_t)n * d * a);
+  w.z = (float*)take((size_t)n * m->NH * 4);
+  w.total = off;
+  return w;
+}
+
 }  // namespace
 
 extern "C" {
@@ -246,6 +431,13 @@ int allie_model_create(const allie_config* cfg, allie_model** out) {
 
 void allie_model_destroy(allie_model* m) {
   if (!m) return;
+  for (int i = 0; i < PinnedRing::N; ++i) {
+    if (m->pinned.ev[i]) {
+      hipEventSynchronize(m->pinned.ev[i]);
+      hipEventDestroy(m->pinned.ev[i]);
+    }
+    if (m->pinned.buf[i]) hipHostFree(m->pinned.buf[i]);
+  }
   if (m->arena) hipFree(m->arena);
   delete m;
 }
@@ -426,6 +618,7 @@ size_t allie_kv_block_bytes(const allie_model* m) {
 int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_host, int n_seq,
                   float temperature, const uint32_t* legal, int legal_words,
                   const allie_outputs* out, void* kv_pool, int kv_pool_blocks, int first_block,
+                  const int32_t* kv_block_table, int kv_max_blocks,
                   void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_ready(m);
   if (rc) return rc;
@@ -444,7 +637,8 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
     n_blocks += (n + KV_BLOCK - 1) / KV_BLOCK;
   }
   if (T > (int64_t)1 << 30) return fail(ALLIE_ERR_ARG, "too many tokens");
-  if (kv_pool && (first_block < 0 || first_block + n_blocks > kv_pool_blocks))
+  if (kv_block_table && kv_max_blocks <= 0) return fail(ALLIE_ERR_ARG, "kv_max_blocks must be positive");
+  if (kv_pool && !kv_block_table && (first_block < 0 || first_block + n_blocks > kv_pool_blocks))
     return fail(ALLIE_ERR_LENGTH, "KV pool too small: need blocks [%d, %lld), have %d", first_block,
                 (long long)(first_block + n_blocks), kv_pool_blocks);
   PrefillWS w = layout_prefill(m, n_seq, (int)T, (char*)workspace);
@@ -454,7 +648,7 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
   const int d = m->d, L = m->L, act = m->act_bf16;
   const float eps = m->cfg.eps;
 
-  HIP_TRY(hipMemcpyAsync(w.lens, lens_host, (size_t)n_seq * 4, hipMemcpyHostToDevice, st));
+  if ((rc = upload_i32(m, w.lens, lens_host, (size_t)n_seq, st))) return rc;
   PackArgs p{};
   p.words = words;
   p.lens = w.lens;
@@ -475,6 +669,8 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
   p.block_table = nullptr;
   p.slot = kv_pool ? w.slot : nullptr;
   p.tiles = w.tiles;
+  p.block_table_in = kv_block_table;
+  p.max_blocks_in = kv_max_blocks;
   p.pad_id = ALLIE_PAD_ID;
   p.status = w.status;
   HIP_TRY(launch_pack(p, st));
@@ -485,6 +681,7 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
   ea.T = (int)T;
   ea.d = d;
   ea.vocab = m->V;
+  ea.n_positions = m->cfg.n_positions;
   ea.wte = m->wte;
   ea.wpe = m->wpe;
   ea.ctrl = m->ctrl;
@@ -509,95 +706,132 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
   aa.out = w.attn;
   aa.act_bf16 = act;
 
-  LNArgs ln{};
-  ln.h = w.h;
-  ln.rows = ln.rows_out = (int)T;
-  ln.d = d;
-  ln.eps = eps;
-  ln.y = w.x;
-  ln.act_bf16 = act;
-
-  const int Ti = (int)T;
-  for (int li = 0; li < L; ++li) {
-    const LayerW& l = m->layers[li];
-    if ((rc = gemm(m, w.x, l.w_qkv, l.b_qkv, l.s_qkv, w.qkv, nullptr, Ti, 3 * d, d, EPI_STORE, ALLIE_PROBE_QKV, st))) return rc;
-    if (kv_pool) {
-      KVWriteArgs kw{};
-      kw.qkv = w.qkv;
-      kw.slot = w.slot;
-      kw.T = Ti;
-      kw.n_layer = L;
-      kw.layer = li;
-      kw.n_head = m->H;
-      kw.head_dim = m->hd;
-      kw.pool = kv_pool;
-      kw.act_bf16 = act;
-      HIP_TRY(launch_kv_write(kw, st));
-    }
-    HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, true, st));
-    HIP_TRY(launch_attn_varlen(aa, st));
-    HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, false, st));
-    if ((rc = gemm(m, w.attn, l.w_o, l.b_o, l.s_o, nullptr, w.h, Ti, d, d, EPI_RESID, ALLIE_PROBE_PROJ, st))) return rc;
-    ln.g = l.ln2_g;
-    ln.b = l.ln2_b;
-    HIP_TRY(launch_layernorm(ln, st));
-    if ((rc = gemm(m, w.x, l.w_fc, l.b_fc, l.s_fc, w.ff, nullptr, Ti, 4 * d, d, EPI_GELU, ALLIE_PROBE_FC, st))) return rc;
-    if ((rc = gemm(m, w.ff, l.w_pr, l.b_pr, l.s_pr, nullptr, w.h, Ti, d, 4 * d, EPI_RESID, ALLIE_PROBE_FC2, st))) return rc;
-    if (li + 1 < L) {
-      ln.g = m->layers[li + 1].ln1_g;
-      ln.b = m->layers[li + 1].ln1_b;
-      HIP_TRY(launch_layernorm(ln, st));
-    }
-  }
+  const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff};
+  rc = run_layers(m, acts, (int)T, kv_pool ? w.slot : nullptr, kv_pool, kv_pool_blocks,
+                  [&](int) -> int {
+                    HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, true, st));
+                    HIP_TRY(launch_attn_varlen(aa, st));
+                    HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, false, st));
+                    return ALLIE_OK;
+                  },
+                  st);
+  if (rc) return rc;
   // heads on the last token of every game
-  LNArgs lf{};
-  lf.h = w.h;
-  lf.row_idx = w.last;
-  lf.rows = lf.rows_out = n_seq;
-  lf.d = d;
-  lf.g = m->lnf_g;
-  lf.b = m->lnf_b;
-  lf.eps = eps;
-  lf.y = w.hx;
-  lf.act_bf16 = act;
-  HIP_TRY(launch_layernorm(lf, st));
-  {
-    GemmArgs g{};
-    g.A = w.hx;
-    g.W = m->w_head;
-    g.bias = m->b_head;
-    g.C = w.z;
-    g.M = n_seq;
-    g.N = m->NH;
-    g.K = d;
-    g.lda = d;
-    g.ldc = m->NH;
-    g.epi = EPI_STORE;
-    g.wtype = act ? W_BF16 : W_F32;
-    g.out_f32 = 1;
-    hipError_t e = launch_gemm(g, st);
-    if (e != hipSuccess) return fail(ALLIE_ERR_HIP, "heads gemm: %s", hipGetErrorString(e));
+  return run_heads(m, w.h, w.last, n_seq, w.hx, w.z, temperature, legal, legal_words, out, st);
+}
+
+size_t allie_extend_workspace_bytes(const allie_model* m, int n_tok, int n_groups) {
+  if (!m || n_tok < 0 || n_groups < 0) return 0;
+  return layout_extend(m, n_tok, n_groups, nullptr).total;
+}
+
+int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_tok,
+                 const int32_t* group_start_host, int n_groups, const int32_t* prefix_len,
+                 const int32_t* prefix_blocks, int max_blocks, const int32_t* extra_slot,
+                 const int32_t* n_extra, int max_extra, float temperature, const uint32_t* legal,
+                 int legal_words, const allie_outputs* out, void* kv_pool, int kv_pool_blocks,
+                 int32_t* status, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_ready(m);
+  if (rc) return rc;
+  if (n_tok <= 0 || n_groups <= 0 || !ids || !pos || !group_start_host || !prefix_len ||
+      !extra_slot || !n_extra || !out || !kv_pool || !workspace || max_extra <= 0 || max_blocks < 0 ||
+      (max_blocks > 0 && !prefix_blocks) || kv_pool_blocks <= 0)
+    return fail(ALLIE_ERR_ARG, "bad extend arguments");
+  if (!out->value || !out->time || !out->top1 || !out->max_logit || !out->lse)
+    return fail(ALLIE_ERR_ARG, "value/time/top1/max_logit/lse outputs are required");
+  if (legal && legal_words * 32 < 1968) return fail(ALLIE_ERR_ARG, "legal mask too narrow");
+  // groups: contiguous, non-empty, covering [0, n_tok); tiles of 64 queries
+  if (group_start_host[0] != 0 || group_start_host[n_groups] != n_tok)
+    return fail(ALLIE_ERR_ARG, "group_start must run from 0 to n_tok");
+  if (n_groups > (1 << 23)) return fail(ALLIE_ERR_ARG, "too many groups");
+  int64_t n_tiles = 0;
+  int max_group = 0;
+  for (int g = 0; g < n_groups; ++g) {
+    const int sz = group_start_host[g + 1] - group_start_host[g];
+    if (sz <= 0) return fail(ALLIE_ERR_ARG, "group %d is empty", g);
+    if (sz > 64 * 256) return fail(ALLIE_ERR_ARG, "group %d has %d tokens (max 16384)", g, sz);
+    max_group = sz > max_group ? sz : max_group;
+    n_tiles += (sz + 63) / 64;
   }
-  HeadsArgs ha{};
-  ha.z = w.z;
-  ha.B = n_seq;
-  ha.ldz = m->NH;
-  ha.vocab = m->V;
-  ha.n_moves = 1968;
-  ha.value_col = m->V;
-  ha.time_col = m->V + 1;
-  ha.temperature = temperature > 1e-5f ? temperature : 1e-5f;
-  ha.legal = legal;
-  ha.legal_words = legal_words;
-  ha.logits = out->logits;
-  ha.value = out->value;
-  ha.time = out->time;
-  ha.top1 = out->top1;
-  ha.lse = out->lse;
-  ha.max_logit = out->max_logit;
-  ha.emulate_bf16 = act;
-  HIP_TRY(launch_heads(ha, st));
-  return ALLIE_OK;
+  ExtendWS w = layout_extend(m, n_tok, n_groups, (char*)workspace);
+  if (workspace_bytes < w.total)
+    return fail(ALLIE_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, w.total);
+  hipStream_t st = (hipStream_t)stream;
+  const int act = m->act_bf16;
+  if ((rc = upload_i32(m, w.group_start, group_start_host, (size_t)n_groups + 1, st))) return rc;
+  // the tree kernel shares a group's prefix across a 64-query tile; groups of
+  // one token (decode) stream it with one wave per query
+  const bool tree = act && max_group > 1;
+  if (tree) HIP_TRY(launch_extend_tiles(w.group_start, n_groups, w.tiles, st));
+
+  ExtendPrepArgs pa{};
+  pa.n = n_tok;
+  pa.n_groups = n_groups;
+  pa.max_blocks = max_blocks;
+  pa.max_extra = max_extra;
+  pa.pool_blocks = kv_pool_blocks;
+  pa.n_positions = m->cfg.n_positions;
+  pa.pos = pos;
+  pa.group_start = w.group_start;
+  pa.prefix_len = prefix_len;
+  pa.prefix_blocks = prefix_blocks;
+  pa.extra_slot = extra_slot;
+  pa.n_extra = n_extra;
+  pa.self_slot = w.self_slot;
+  pa.status = status ? status : w.status;
+  HIP_TRY(launch_extend_prepare(pa, st));
+
+  EmbedArgs ea{};
+  ea.ids = ids;
+  ea.pos = pos;
+  ea.T = n_tok;
+  ea.d = m->d;
+  ea.vocab = m->V;
+  ea.n_positions = m->cfg.n_positions;
+  ea.wte = m->wte;
+  ea.wpe = m->wpe;
+  ea.ctrl = m->ctrl;
+  ea.ln_g = m->layers[0].ln1_g;
+  ea.ln_b = m->layers[0].ln1_b;
+  ea.eps = m->cfg.eps;
+  ea.h = w.h;
+  ea.x = w.x;
+  ea.act_bf16 = act;
+  HIP_TRY(launch_embed_ln(ea, st));
+
+  ExtendAttnArgs xa{};
+  xa.qkv = w.qkv;
+  xa.n = n_tok;
+  xa.n_head = m->H;
+  xa.group_start = w.group_start;
+  xa.n_groups = n_groups;
+  xa.prefix_len = prefix_len;
+  xa.prefix_blocks = prefix_blocks;
+  xa.max_blocks = max_blocks;
+  xa.extra_slot = extra_slot;
+  xa.n_extra = n_extra;
+  xa.max_extra = max_extra;
+  xa.tiles = w.tiles;
+  xa.n_tiles = (int)n_tiles;
+  xa.pool = kv_pool;
+  xa.pool_blocks = kv_pool_blocks;
+  xa.n_layer = m->L;
+  xa.scale = 0.125f;  // 1 / sqrt(64)
+  xa.out = w.attn;
+  xa.act_bf16 = act;
+
+  const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff};
+  rc = run_layers(m, acts, n_tok, w.self_slot, kv_pool, kv_pool_blocks,
+                  [&](int layer) -> int {
+                    xa.layer = layer;
+                    HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, true, st));
+                    HIP_TRY(tree ? launch_attn_extend_tree(xa, st) : launch_attn_extend_wave(xa, st));
+                    HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, false, st));
+                    return ALLIE_OK;
+                  },
+                  st);
+  if (rc) return rc;
+  return run_heads(m, w.h, nullptr, n_tok, w.hx, w.z, temperature, legal, legal_words, out, st);
 }
 
 int allie_probe_begin(int kind, int max_launches) {

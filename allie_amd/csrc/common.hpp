@@ -23,6 +23,23 @@ ALLIE_DEV float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
 ALLIE_DEV float round_bf16(float f) { return bf2f(f2bf(f)); }
 ALLIE_DEV uint32_t pack_bf16x2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
 
+// Elements OFF .. OFF+7 of x -> hi = bf16(x), lo = bf16(x - hi): hi + lo
+// carries ~16 mantissa bits of x (for MFMA operands that need more than
+// bf16's 8).
+template <int OFF>
+ALLIE_DEV void split_bf16x8(const f32x16_t& x, bf16x8_t& hi, bf16x8_t& lo) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float x0 = x[OFF + 2 * e], x1 = x[OFF + 2 * e + 1];
+    const uint32_t h0 = f2bf(x0), h1 = f2bf(x1);
+    h[e] = h0 | (h1 << 16);
+    l[e] = pack_bf16x2(x0 - bf2f(h0), x1 - bf2f(h1));
+  }
+  hi = __builtin_bit_cast(bf16x8_t, u32x4_t{h[0], h[1], h[2], h[3]});
+  lo = __builtin_bit_cast(bf16x8_t, u32x4_t{l[0], l[1], l[2], l[3]});
+}
+
 // OCP fp8 e4m3fn -> fp32 (exact).  bias 7, no infinities, 0x7f/0xff = NaN.
 ALLIE_DEV float fp8e4m3_to_f32(uint32_t v) {
   uint32_t s = (v & 0x80u) << 24;

@@ -20,6 +20,8 @@ struct PackArgs {
   int32_t* blk_off;       // [B+1]
   int32_t* block_table;   // [B][max_blocks] or null
   int32_t* slot;          // [T] or null
+  const int32_t* block_table_in;  // optional [B][max_blocks_in]: slots come from these blocks
+  int max_blocks_in;
   int32_t* tiles;         // attention query tiles or null
   int pad_id;             // token id flagged when it occurs inside a game (-1: none)
   int32_t* status;        // [1]: bit 1 empty game, 2 capacity exceeded, 4 table too small,
@@ -34,6 +36,7 @@ struct EmbedArgs {
   const int32_t* ids;
   const int32_t* pos;
   int T, d, vocab;
+  int n_positions;    // rows of wpe; positions are clamped into [0, n_positions)
   const float* wte;   // [vocab][d]
   const float* wpe;   // [n_pos][d]
   const float* ctrl;  // [2][d]
@@ -104,43 +107,64 @@ hipError_t launch_attn_varlen(const AttnVarlenArgs& a, hipStream_t st);
 constexpr int KV_BLOCK = 16;
 struct KVWriteArgs {
   const void* qkv;       // [T][3d]
-  const int32_t* slot;   // [T]
+  const int32_t* slot;   // [T] pool slot (block * 16 + offset); invalid slots are skipped
   int T, n_layer, layer, n_head, head_dim;
+  int pool_blocks;       // blocks in the pool (bounds of every slot)
   void* pool;
   int act_bf16;
 };
 hipError_t launch_kv_write(const KVWriteArgs& a, hipStream_t st);
 
-struct AttnPagedArgs {
-  const void* qkv;            // [T][3d]: queries of the new tokens
-  const int32_t* q_seq;       // [T] sequence of each query
-  const int32_t* q_pos;       // [T] position of each query (keys 0..pos visible)
-  const int32_t* block_table; // [B][max_blocks]
-  int max_blocks, T, n_head, head_dim;
-  const void* pool;           // layer base
+// Extend attention: n new tokens, in groups (tokens of group g are
+// [group_start[g], group_start[g+1])).  Token i of group g attends
+//   1. the group's shared prefix: positions 0 .. prefix_len[g]-1, held in the
+//      pool blocks prefix_blocks[g][0 ..], and then
+//   2. its private keys: the n_extra[i] pool slots extra_slot[i][0 ..] (a
+//      search node's ancestors, then the token itself).
+// Every key is visible (the causal order is in how the caller builds the
+// lists).  Pool layout: [block][layer][k|v][head][16][head_dim].  Block ids
+// and slots outside the pool are skipped (and flagged by extend_prepare).
+struct ExtendAttnArgs {
+  const void* qkv;             // [n][3d] new tokens (q | k | v)
+  int n, n_head;
+  const int32_t* group_start;  // [G + 1]
+  int n_groups;
+  const int32_t* prefix_len;   // [G]
+  const int32_t* prefix_blocks;  // [G][max_blocks]
+  int max_blocks;
+  const int32_t* extra_slot;   // [n][max_extra]
+  const int32_t* n_extra;      // [n]
+  int max_extra;
+  const int32_t* tiles;        // MFMA kernel: (group << 8) | q_tile of 64 queries
+  int n_tiles;
+  const void* pool;            // pool base (the kernel adds the layer offset)
+  int pool_blocks, n_layer, layer;
   float scale;
-  void* out;                  // [T][d]
+  void* out;                   // [n][d]
   int act_bf16;
 };
-hipError_t launch_attn_paged(const AttnPagedArgs& a, hipStream_t st);
+// one wave per (token, head), any group sizes, bf16 or fp32
+hipError_t launch_attn_extend_wave(const ExtendAttnArgs& a, hipStream_t st);
+// MFMA tiles of 64 queries sharing a group's prefix (bf16); needs tiles
+hipError_t launch_attn_extend_tree(const ExtendAttnArgs& a, hipStream_t st);
+// tiles[] = (g << 8) | t for every 64-query tile t of every group g, in order
+hipError_t launch_extend_tiles(const int32_t* group_start, int n_groups, int32_t* tiles, hipStream_t st);
 
-// Tree attention: node i attends its root's shared prefix (paged) and its own
-// ancestor chain (node slots), then itself.
-struct AttnTreeArgs {
-  const void* qkv;             // [N][3d] new node tokens
-  const int32_t* root_of;      // [N]
-  const int32_t* block_table;  // [R][max_blocks] prefix blocks per root
-  const int32_t* prefix_len;   // [R]
-  const int32_t* anc_slot;     // [N][max_depth] pool slots of ancestors (root-side first), then self
-  const int32_t* n_anc;        // [N] entries used in anc_slot (ancestors + self)
-  const int32_t* group_start;  // [G+1] nodes grouped by root: tiles never straddle roots
-  int n_groups, max_blocks, max_depth, N, n_head, head_dim;
-  const void* pool;
-  float scale;
-  void* out;
-  int act_bf16;
+// Validates an extend batch and derives each token's own pool slot (the last
+// of its extras).  status bits: 1 n_extra outside [1, max_extra], 2 a block id
+// or slot outside the pool, 4 a position outside [0, n_positions).
+struct ExtendPrepArgs {
+  int n, n_groups, max_blocks, max_extra, pool_blocks, n_positions;
+  const int32_t* pos;
+  const int32_t* group_start;
+  const int32_t* prefix_len;
+  const int32_t* prefix_blocks;
+  const int32_t* extra_slot;
+  const int32_t* n_extra;
+  int32_t* self_slot;          // [n]
+  int32_t* status;             // [1], written (not accumulated)
 };
-hipError_t launch_attn_tree(const AttnTreeArgs& a, hipStream_t st);
+hipError_t launch_extend_prepare(const ExtendPrepArgs& a, hipStream_t st);
 
 // ----------------------------------------------------------------- heads
 // logits/value/time from the heads GEMM output rows, plus softmax summary.

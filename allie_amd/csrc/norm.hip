@@ -62,7 +62,8 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(allie::EmbedArgs a) {
   const int lane = threadIdx.x & 63;
   const int d = a.d;
   const int id = a.ids[t];
-  const int p = a.pos[t];
+  int p = a.pos[t];  // out-of-range positions are flagged by the caller; never read past wpe
+  p = p < 0 ? 0 : (p >= a.n_positions ? a.n_positions - 1 : p);
   const bool elo = id >= a.vocab;
   float e = 0.f, e1 = 0.f;
   if (elo) {

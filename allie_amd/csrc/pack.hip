@@ -122,7 +122,7 @@ __global__ __launch_bounds__(256) void pack_fill_kernel(
     const int64_t* __restrict__ in_off, const int32_t* __restrict__ blk_off,
     int32_t* __restrict__ ids, int32_t* __restrict__ pos, int32_t* __restrict__ seq_of,
     int32_t* __restrict__ block_table, int32_t* __restrict__ slot, int capacity, int pad_id,
-    int32_t* __restrict__ status) {
+    int32_t* __restrict__ status, const int32_t* __restrict__ table_in, int max_blocks_in) {
   const int s = blockIdx.x;
   int n = lens[s] < max_len ? lens[s] : max_len;
   if (n < 0) n = 0;
@@ -142,11 +142,21 @@ __global__ __launch_bounds__(256) void pack_fill_kernel(
     ids[t0 + j] = id;
     pos[t0 + j] = j;
     seq_of[t0 + j] = s;
-    if (slot != nullptr) slot[t0 + j] = (b0 + j / block) * block + j % block;
+    if (slot != nullptr) {
+      if (table_in != nullptr) {  // the caller's blocks for this game (-1: no block, not written)
+        const int bi = j / block;
+        const int b = bi < max_blocks_in ? table_in[(int64_t)s * max_blocks_in + bi] : -1;
+        slot[t0 + j] = b >= 0 ? b * block + j % block : -1;
+      } else {
+        slot[t0 + j] = (b0 + j / block) * block + j % block;
+      }
+    }
   }
   // a PAD id inside a game would be a masked key in the reference's padded
   // batch (data.py:321) but is an ordinary token here: flag it
   if (__syncthreads_or(pad_seen) && threadIdx.x == 0 && status != nullptr) atomicOr(status, 8);
+  // the caller's block table is too short for this game: its tail is not cached
+  if (table_in != nullptr && nb > max_blocks_in && threadIdx.x == 0 && status != nullptr) atomicOr(status, 4);
 }
 
 }  // namespace
@@ -163,7 +173,7 @@ hipError_t launch_pack(const PackArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(pack_fill_kernel, dim3(a.B), dim3(256), 0, st, a.words, a.lens, a.B,
                        a.max_len, a.block, a.first_block, a.max_blocks, a.cu_seqlens, a.in_off,
                        a.blk_off, a.ids, a.pos, a.seq_of, a.block_table, a.slot, a.capacity,
-                       a.pad_id, a.status);
+                       a.pad_id, a.status, a.block_table_in, a.max_blocks_in);
     e = hipGetLastError();
   }
   return e;

@@ -131,6 +131,7 @@ class Engine:
     # -------------------------------------------------------------- prefill
     def prefill(self, words, lens, temperature: float = 1.0, legal=None, want_logits: bool = True,
                 kv_pool: Optional[torch.Tensor] = None, first_block: int = 0,
+                kv_block_table: Optional[torch.Tensor] = None,
                 out: Optional[PrefillResult] = None) -> PrefillResult:
         """Forward of B games given as tokenizer words.
 
@@ -138,6 +139,10 @@ class Engine:
         tensor of int32/uint32 bits); lens: words per game (host ints).
         legal: optional [B, 62] int32 bitmask over move ids (bit i of word
         i // 32) restricting top1 / lse.
+        kv_pool: optional KV pool (``new_kv_pool``) that receives every
+        layer's keys and values: game i's position p goes to block
+        ``kv_block_table[i, p // 16]`` (device int32 [B, max_blocks]) if that
+        table is given, else to the contiguous blocks from ``first_block``.
         """
         lens_np = np.ascontiguousarray(np.asarray(lens, dtype=np.int32))
         B = len(lens_np)
@@ -167,13 +172,81 @@ class Engine:
             kv_blocks = 0
             if kv_pool is not None:
                 kv_blocks = kv_pool.numel() * kv_pool.element_size() // self.kv_block_bytes()
+            kv_max_blocks = 0
+            if kv_block_table is not None:
+                assert kv_block_table.dtype == torch.int32 and kv_block_table.is_contiguous()
+                assert kv_block_table.shape[0] == B
+                kv_max_blocks = kv_block_table.shape[1]
             rc = self._lib.allie_prefill(
                 self._m, capi.ptr(wd), lens_np.ctypes.data_as(C.c_void_p), B, float(temperature),
                 capi.ptr(legal_t), LEGAL_WORDS if legal_t is not None else 0, C.byref(o),
-                capi.ptr(kv_pool), int(kv_blocks), int(first_block), capi.ptr(ws), ws.numel(),
-                capi.stream_ptr(),
+                capi.ptr(kv_pool), int(kv_blocks), int(first_block), capi.ptr(kv_block_table),
+                int(kv_max_blocks), capi.ptr(ws), ws.numel(), capi.stream_ptr(),
             )
             capi.check(rc, "allie_prefill")
+        return out
+
+    # ------------------------------------------------------------- KV cache
+    def new_kv_pool(self, n_blocks: int) -> torch.Tensor:
+        """Device KV pool of n_blocks blocks of 16 positions (every layer's
+        keys and values, layout [block][layer][k|v][head][16][64])."""
+        return torch.empty(n_blocks * self.kv_block_bytes(), dtype=torch.uint8, device=self.device)
+
+    def pool_blocks(self, kv_pool: torch.Tensor) -> int:
+        return kv_pool.numel() * kv_pool.element_size() // self.kv_block_bytes()
+
+    # --------------------------------------------------------------- extend
+    def extend(self, ids, pos, group_sizes, prefix_len, prefix_blocks, extra_slot, n_extra,
+               kv_pool: torch.Tensor, temperature: float = 1.0, legal=None, want_logits: bool = True,
+               status: Optional[torch.Tensor] = None, out: Optional[PrefillResult] = None) -> PrefillResult:
+        """Forward of n new tokens over the paged KV cache (decode steps, MCTS
+        tree levels).  Tokens come in groups of ``group_sizes`` (host ints);
+        token i of group g attends the group's prefix (``prefix_len[g]``
+        positions in blocks ``prefix_blocks[g]``) and then its own pool slots
+        ``extra_slot[i, :n_extra[i]]``, the last of which receives its keys and
+        values.  Array arguments are device int32 tensors (or numpy, copied).
+        Returns per-token outputs like ``prefill``."""
+        dev = self.device
+
+        def dt(a, shape=None):
+            t = a if isinstance(a, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32))
+            t = t.to(device=dev, dtype=torch.int32).contiguous()
+            return t if shape is None else t.reshape(shape)
+
+        gs = np.asarray(group_sizes, dtype=np.int64)
+        G = len(gs)
+        n = int(gs.sum())
+        group_start = np.zeros(G + 1, dtype=np.int32)
+        group_start[1:] = np.cumsum(gs)
+        ids_t, pos_t = dt(ids), dt(pos)
+        pl_t = dt(prefix_len)
+        pb_t = dt(prefix_blocks)
+        pb_t = pb_t.reshape(G, -1) if pb_t.numel() else pb_t.reshape(G, 0)
+        es_t = dt(extra_slot).reshape(n, -1)
+        ne_t = dt(n_extra)
+        assert ids_t.numel() == n and pos_t.numel() == n and ne_t.numel() == n and pl_t.numel() == G
+        if out is None:
+            f = lambda: torch.empty(n, dtype=torch.float32, device=dev)
+            out = PrefillResult(
+                logits=torch.empty(n, self.cfg.vocab_size, dtype=torch.float32, device=dev) if want_logits else None,
+                value=f(), time=f(), top1=torch.empty(n, dtype=torch.int32, device=dev), max_logit=f(), lse=f(),
+            )
+        o = capi.AllieOutputs(capi.ptr(out.logits).value, capi.ptr(out.value).value, capi.ptr(out.time).value,
+                              capi.ptr(out.top1).value, capi.ptr(out.max_logit).value, capi.ptr(out.lse).value)
+        with torch.cuda.device(dev):
+            ws = self._workspace(int(self._lib.allie_extend_workspace_bytes(self._m, n, G)))
+            legal_t = None
+            if legal is not None:
+                legal_t = _as_tensor(legal).to(torch.int32).to(dev).contiguous()
+                assert legal_t.shape == (n, LEGAL_WORDS)
+            rc = self._lib.allie_extend(
+                self._m, capi.ptr(ids_t), capi.ptr(pos_t), n, group_start.ctypes.data_as(C.c_void_p), G,
+                capi.ptr(pl_t), capi.ptr(pb_t), pb_t.shape[1], capi.ptr(es_t), capi.ptr(ne_t), es_t.shape[1],
+                float(temperature), capi.ptr(legal_t), LEGAL_WORDS if legal_t is not None else 0, C.byref(o),
+                capi.ptr(kv_pool), self.pool_blocks(kv_pool), capi.ptr(status), capi.ptr(ws), ws.numel(),
+                capi.stream_ptr(),
+            )
+            capi.check(rc, "allie_extend")
         return out
 
     def close(self) -> None:

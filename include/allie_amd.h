@@ -139,14 +139,48 @@ typedef struct allie_outputs {
  * legal: optional [n_seq][legal_words] bitmask over move ids (NULL = all).
  * kv_pool: optional paged KV pool of kv_pool_blocks blocks (layout
  * [block][layer][k|v][head][16][head_dim], activation dtype) that receives
- * every layer's keys and values; game i takes the contiguous blocks
- * first_block + blk_off[i] ... (NULL = no cache). */
+ * every layer's keys and values (NULL = no cache).  Game i's position p goes
+ * to block kv_block_table[i][p / 16] (device int32 [n_seq][kv_max_blocks],
+ * entries -1 or outside the pool are not written) when that table is given,
+ * else to the contiguous blocks first_block + blk_off[i] ... */
 size_t allie_prefill_workspace_bytes(const allie_model* m, int n_seq, int n_tokens);
 size_t allie_kv_block_bytes(const allie_model* m);
 int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_host, int n_seq,
                   float temperature, const uint32_t* legal, int legal_words,
                   const allie_outputs* out, void* kv_pool, int kv_pool_blocks, int first_block,
+                  const int32_t* kv_block_table, int kv_max_blocks,
                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* Extend: the forward of n_tok NEW tokens over a paged KV cache -- one
+ * decode step of many games, or one level of MCTS children.  Replaces the
+ * full-prefix recompute that MCTS.evaluate_node runs per leaf
+ * (src/evaluation/decode.py:356-373, "no kv caching", README.md:80) and that
+ * Policy.score_full runs per appended move (decode.py:199-203): the result at
+ * a new token equals that recompute's last-token output.
+ *
+ * Tokens come in n_groups contiguous groups: group g is tokens
+ * [group_start_host[g], group_start_host[g+1]) (HOST array, read during the
+ * call).  Token i of group g attends
+ *   1. the group's shared prefix, positions 0 .. prefix_len[g]-1, stored in
+ *      the pool blocks prefix_blocks[g][0 .. ceil(prefix_len[g]/16)-1], then
+ *   2. its own keys: pool slots extra_slot[i][0 .. n_extra[i]-1] (a search
+ *      node's ancestors in root-to-leaf order, then the node itself).
+ * Every layer's key/value of token i is written to pool slot
+ * extra_slot[i][n_extra[i]-1] (slot = block * 16 + offset) before attention.
+ * ids/pos: the token id and its position (0-based, = number of keys before
+ * it).  All of ids, pos, prefix_len, prefix_blocks, extra_slot, n_extra are
+ * device int32 arrays; outputs are per token as in allie_prefill.
+ * status (device int32[1], optional) is written with 1 a token's n_extra
+ * outside [1, max_extra], 2 a block id or slot outside the pool, 4 a position
+ * outside the model's positions; keys in bad blocks are skipped, never read.
+ * Groups may hold at most 16384 tokens. */
+size_t allie_extend_workspace_bytes(const allie_model* m, int n_tok, int n_groups);
+int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_tok,
+                 const int32_t* group_start_host, int n_groups, const int32_t* prefix_len,
+                 const int32_t* prefix_blocks, int max_blocks, const int32_t* extra_slot,
+                 const int32_t* n_extra, int max_extra, float temperature, const uint32_t* legal,
+                 int legal_words, const allie_outputs* out, void* kv_pool, int kv_pool_blocks,
+                 int32_t* status, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Kernel probe for benchmarks: while active, every launch of one kernel kind
  * inside allie_prefill is bracketed by HIP events on its stream;

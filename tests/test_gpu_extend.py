@@ -1,0 +1,139 @@
+"""Parity of the paged-KV extend path (decode steps and MCTS tree levels).
+
+The reference evaluates every leaf and every appended move by a full
+recompute of the game at batch 1 (src/evaluation/decode.py:356-360,
+199-203); the oracle here is exactly that: ``RefModel.forward_last`` over each
+token's whole sequence (game prefix + ancestors + the token).  The engine
+instead prefills the prefixes into a paged KV pool once and evaluates new
+tokens with ``Engine.extend`` over cached keys and values.  Bars as for the
+prefill: 1e-4 in the fp32 check mode, 2e-2 in bf16, top-1 identical where the
+oracle's top-2 margin exceeds twice the observed logit error.
+"""
+import numpy as np
+import pytest
+import torch
+
+from allie_amd import config, weights
+from allie_amd.engine import Engine
+from oracle.model_ref import RefModel, policy_summary
+
+pytestmark = pytest.mark.gpu
+
+BPG = 8  # pool blocks owned by each game / root in these tests (128 positions)
+
+
+def check(got, ref, tol, what):
+    lg = got.logits.cpu().numpy()
+    dl = float(np.abs(lg - ref["logits"]).max())
+    dv = float(np.abs(got.value.cpu().numpy() - ref["value_logits"]).max())
+    dt = float(np.abs(got.time.cpu().numpy() - ref["time_logits"]).max())
+    assert dl <= tol and dv <= tol and dt <= tol, (what, dl, dv, dt)
+    ps = policy_summary(ref["logits"])
+    need = ps["margin"] > max(2 * dl, 1e-6)
+    top1 = got.top1.cpu().numpy()
+    assert (top1[need] == ps["top1"][need]).all(), (what, np.nonzero(top1 != ps["top1"]))
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    cfg = config.TINY
+    return cfg, weights.init_weights(cfg, seed=11, perturb=True)
+
+
+@pytest.mark.parametrize("mode,tol", [("float32", 1e-4), ("bfloat16", 2e-2)])
+def test_decode_steps_match_full_recompute(tiny, mode, tol, cuda):
+    cfg, sd = tiny
+    rng = np.random.default_rng(5)
+    B = 9
+    lens = rng.integers(1, 70, B).astype(np.int32)
+    seqs = [list(rng.integers(0, 1968, n)) for n in lens]
+    eng = Engine(cfg, sd, mode=mode)
+    pool = eng.new_kv_pool(B * BPG + 3)
+    # game b owns blocks 3 + b * BPG ...: a non-contiguous, non-zero layout
+    table = torch.tensor([[3 + b * BPG + j for j in range(BPG)] for b in range(B)], dtype=torch.int32, device=cuda)
+    words = np.concatenate([np.asarray(s, np.uint32) for s in seqs])
+    eng.prefill(words, lens, kv_pool=pool, kv_block_table=table)
+    oracle = RefModel(cfg, sd, mode=mode)
+    status = torch.full((1,), -1, dtype=torch.int32, device=cuda)
+    for step in range(3):
+        new = rng.integers(0, 1968, B)
+        cur = np.array([len(s) for s in seqs], np.int32)  # position of the new token
+        slots = np.array([(3 + b * BPG + cur[b] // 16) * 16 + cur[b] % 16 for b in range(B)], np.int32)
+        out = eng.extend(new, cur, [1] * B, cur, table, slots[:, None], np.ones(B, np.int32), pool, status=status)
+        torch.cuda.synchronize()
+        assert int(status.item()) == 0
+        for b in range(B):
+            seqs[b].append(int(new[b]))
+        ref = oracle.forward_last([np.asarray(s, np.int64) for s in seqs])
+        check(out, ref, tol, f"{mode} decode step {step}")
+    eng.close()
+
+
+@pytest.mark.parametrize("mode,tol", [("float32", 1e-4), ("bfloat16", 2e-2)])
+def test_tree_levels_match_full_recompute(tiny, mode, tol, cuda):
+    """Roots with shared prefixes; level-1 children (one root has 70, which
+    spans two 64-query tiles) and level-2 grandchildren that see the prefix,
+    their parent and themselves."""
+    cfg, sd = tiny
+    rng = np.random.default_rng(9)
+    prefix = [37, 64, 100]
+    kids = [3, 70, 5]
+    R = len(prefix)
+    roots = [list(rng.integers(0, 1968, n)) for n in prefix]
+    eng = Engine(cfg, sd, mode=mode)
+    node_base = R * BPG  # node slots live in the blocks after the roots'
+    n1 = sum(kids)
+    pool = eng.new_kv_pool(node_base + (3 * n1 + 15) // 16 + 1)
+    table = torch.tensor([[r * BPG + j for j in range(BPG)] for r in range(R)], dtype=torch.int32, device=cuda)
+    eng.prefill(np.concatenate([np.asarray(s, np.uint32) for s in roots]), np.array(prefix, np.int32),
+                kv_pool=pool, kv_block_table=table)
+    oracle = RefModel(cfg, sd, mode=mode)
+    status = torch.zeros(1, dtype=torch.int32, device=cuda)
+
+    # level 1: one token per child, extras = [own slot]
+    ids1 = rng.integers(0, 1968, n1)
+    slot1 = node_base * 16 + np.arange(n1, dtype=np.int32)
+    root_of1 = np.repeat(np.arange(R), kids)
+    pos1 = np.array([prefix[r] for r in root_of1], np.int32)
+    out1 = eng.extend(ids1, pos1, kids, prefix, table, slot1[:, None], np.ones(n1, np.int32), pool, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    paths1 = [roots[root_of1[i]] + [int(ids1[i])] for i in range(n1)]
+    check(out1, oracle.forward_last([np.asarray(p, np.int64) for p in paths1]), tol, f"{mode} level 1")
+
+    # level 2: two children for every level-1 node, extras = [parent, own slot]
+    par = np.repeat(np.arange(n1), 2)
+    n2 = len(par)
+    ids2 = rng.integers(0, 1968, n2)
+    slot2 = node_base * 16 + n1 + np.arange(n2, dtype=np.int32)
+    extra = np.stack([slot1[par], slot2], axis=1).astype(np.int32)
+    pos2 = pos1[par] + 1
+    sizes2 = [2 * k for k in kids]  # grouped by root, in order
+    out2 = eng.extend(ids2, pos2, sizes2, prefix, table, extra, np.full(n2, 2, np.int32), pool, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    paths2 = [paths1[par[i]] + [int(ids2[i])] for i in range(n2)]
+    check(out2, oracle.forward_last([np.asarray(p, np.int64) for p in paths2]), tol, f"{mode} level 2")
+    eng.close()
+
+
+def test_extend_status_flags(tiny, cuda):
+    """Bad slots, counts and positions are flagged and never dereferenced."""
+    cfg, sd = tiny
+    eng = Engine(cfg, sd, mode="bfloat16")
+    pool = eng.new_kv_pool(4)
+    status = torch.zeros(1, dtype=torch.int32, device=cuda)
+    table = np.zeros((1, 2), np.int32)
+    # slot in block 9 of a 4-block pool
+    eng.extend([5], [3], [1], [3], table, [[9 * 16 + 2]], [1], pool, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) & 2
+    # n_extra = 0
+    eng.extend([5], [3], [1], [3], table, [[1]], [0], pool, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) & 1
+    # position past the model's positions; prefix block id -1
+    eng.extend([5], [5000], [1], [3], np.full((1, 2), -1, np.int32), [[1]], [1], pool, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) & 4 and int(status.item()) & 2
+    eng.close()

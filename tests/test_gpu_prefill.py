@@ -45,6 +45,7 @@ def check(got, ref, tol, mode):
     dl = np.abs(got["logits"] - ref["logits"]).max()
     dv = np.abs(got["value"] - ref["value_logits"]).max()
     dt = np.abs(got["time"] - ref["time_logits"]).max()
+    print(f"{mode}: max|dlogit|={dl:.3g} max|dvalue|={dv:.3g} max|dtime|={dt:.3g} (tol {tol})", flush=True)
     assert dl <= tol and dv <= tol and dt <= tol, (mode, dl, dv, dt)
     ps = policy_summary(ref["logits"])
     need = ps["margin"] > max(2 * dl, 1e-6)
