@@ -1,21 +1,28 @@
 """Benchmark of the batched policy/value inference path on one MI355X.
 
-Default workload (the headline metric's configuration): medium shape
-(24 layers, d_model 1024, 16 heads), bf16, one ragged packed batch of 256
-game prefixes with lengths ``default_rng(2).integers(8, 401, 256)`` and
-uniform move-token ids; one step = one prefill forward emitting policy
-logits, value and time at every game's last token.  ``value`` is leaf
+``python bench.py`` (the driver's line) measures the headline configuration:
+medium shape (24 layers, d_model 1024, 16 heads), bf16, one ragged packed
+batch of 256 game prefixes with lengths ``default_rng(2).integers(8, 401,
+256)`` and uniform move-token ids; one step = one prefill forward emitting
+policy logits, value and time at every game's last token.  ``value`` is leaf
 (prefix) evaluations per second with the inputs already resident in HBM.
 
-Also reported, on the same JSON line:
+On the same JSON line:
 * ``roofline`` for the dominant kernel (the MLP c_fc GEMM + gelu): its
   algorithmic FLOPs per launch (2 * T * 4096 * 1024) over its average launch
   duration, measured with HIP events around each of its launches inside the
-  timed forwards, against the dense bf16 MFMA peak;
+  timed forwards (on the stream they run on), against the dense bf16 MFMA
+  peak; ``traffic`` is the copy-calibrated HBM bytes per launch from the
+  committed rocprofv3 counter summary;
 * ``cpu_baseline``: the CPU oracle (fp32, the reference's execution shape:
   one B=1 forward per game as Policy.score_full / MCTS.evaluate_node do,
   src/evaluation/decode.py:199-203,356-360) timed on a bounded sample of the
   same games on the host cores.
+
+``--config c3|c4|c5`` measures the other synthetic workloads, one JSON line
+each: MCTS tree expansion (leaf evals/s), continuous-batching self-play
+decode (tokens/s and step latency), and the fp8-weight 2x model (leaf
+evals/s, top-1 agreement with bf16).
 """
 from __future__ import annotations
 
@@ -33,6 +40,8 @@ sys.path.insert(0, ROOT)
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 HBM_PEAK_GBS = 8000.0
+METRIC = "leaf evals/sec @ medium, ragged batch 256; % of MFMA / HBM roofline"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gemm_fc_c2.txt")
 
 
 def c2_batch():
@@ -50,47 +59,6 @@ def alg_flops(cfg, lens):
     attn = 2 * cfg.n_layer * cfg.d_model * int(np.sum(lens.astype(np.int64) * (lens + 1)))
     heads = 2 * len(lens) * cfg.d_model * (cfg.vocab_size + 2)
     return 2 * P * T + attn + heads
-
-
-def cpu_baseline(cfg, sd, seqs, budget_s: float = 20.0):
-    import torch
-
-    from oracle.model_ref import RefModel
-
-    cores = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(cores)
-    ref = RefModel(cfg, sd, mode="float32")
-    # one warm-up game, then B=1 forwards (as Policy.score_full calls the model)
-    ids0 = torch.as_tensor(seqs[0].astype(np.int64))[None]
-    ref.forward_padded(ids0)
-    done, t0 = 0, time.perf_counter()
-    for s in seqs:
-        ref.forward_padded(torch.as_tensor(s.astype(np.int64))[None])
-        done += 1
-        if time.perf_counter() - t0 > budget_s:
-            break
-    el = time.perf_counter() - t0
-    cpu_model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    return {
-        "value": done / el,
-        "unit": "leaf evals/s",
-        "cores": cores,
-        "kind": "port",
-        "sample": f"first {done} games of the same batch, one fp32 B=1 forward each "
-                  f"(all-position logits, no KV cache), {el:.1f} s; cpu {cpu_model!r}; "
-                  f"torch {torch.__version__}",
-    }
-
-
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gemm_fc_c2.txt")
 
 
 def read_traffic():
@@ -119,11 +87,279 @@ def calibrate_copy(mib: int = 512, reps: int = 3):
     print(json.dumps({"calibration_copy_bytes": x.numel(), "reps": reps}), flush=True)
 
 
+def cpu_baseline(cfg, sd, seqs, budget_s: float = 20.0):
+    import torch
+
+    from oracle.model_ref import RefModel
+
+    cores = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    ref = RefModel(cfg, sd, mode="float32")
+    # one warm-up game, then B=1 forwards (as Policy.score_full calls the model)
+    ref.forward_padded(torch.as_tensor(seqs[0].astype(np.int64))[None])
+    done, t0 = 0, time.perf_counter()
+    for s in seqs:
+        ref.forward_padded(torch.as_tensor(s.astype(np.int64))[None])
+        done += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    el = time.perf_counter() - t0
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": done / el,
+        "unit": "leaf evals/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"first {done} games of the same batch, one fp32 B=1 forward each "
+                  f"(all-position logits, no KV cache), {el:.1f} s; cpu {cpu_model!r}; "
+                  f"torch {torch.__version__}",
+    }
+
+
+class Probe:
+    """HIP events around every launch of one kernel kind inside the engine's
+    calls (recorded on the stream the kernels run on)."""
+
+    def __init__(self, kind, max_launches):
+        from allie_amd import capi
+
+        self.capi = capi
+        capi.check(capi.lib().allie_probe_begin(kind, max_launches), "probe")
+
+    def end(self):
+        tot, n = C.c_float(), C.c_int()
+        self.capi.check(self.capi.lib().allie_probe_end(C.byref(tot), C.byref(n)), "probe end")
+        return tot.value, n.value
+
+
+def base_result(args, value, unit, ms, dtype, workload, **config):
+    return {
+        "metric": METRIC, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": dtype,
+        "data": "synthetic (seeded inputs, random-init GPT-2 weights)",
+        "config": {"workload": workload, **config, "parallelism": "single GPU"},
+    }
+
+
+# ------------------------------------------------------------------- C2 / C5
+def run_prefill(args, cfg, mode, workload):
+    import torch
+
+    from allie_amd import capi, weights
+    from allie_amd.engine import Engine
+
+    sd = weights.init_weights(cfg, seed=0)
+    seqs, lens = c2_batch()
+    T = int(lens.sum())
+    eng = Engine(cfg, sd, mode=mode, device="cuda:0")
+    words = torch.from_numpy(np.concatenate(seqs).view(np.int32)).cuda()
+    out = eng.prefill(words, lens)
+    for _ in range(args.warmup):
+        eng.prefill(words, lens, out=out)
+    torch.cuda.synchronize()
+    probe = Probe(capi.PROBE_FC, args.steps * cfg.n_layer)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        eng.prefill(words, lens, out=out)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    fc_tot, fc_n = probe.end()
+    ms = el * 1000.0 / args.steps
+    flops = alg_flops(cfg, lens)
+    fc_flops = 2.0 * T * cfg.d_ff * cfg.d_model
+    fc_ms = fc_tot / max(fc_n, 1)
+    fc_tflops = fc_flops / (fc_ms * 1e-3) / 1e12
+    res = base_result(args, len(lens) / (ms / 1000.0), "leaf evals/s", ms,
+                      "bf16" if mode == "bfloat16" else "fp8 e4m3 weights, bf16 activations", workload,
+                      n_seq=len(lens), n_tokens=T, tokens_per_s=T / (ms / 1000.0),
+                      alg_tflop_per_step=flops / 1e12,
+                      whole_forward_mfma_frac=flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS)
+    res["roofline"] = {
+        "kernel": f"gemm_mfma_kernel<EPI_GELU,{'W_BF16' if mode == 'bfloat16' else 'W_FP8'}> (MLP c_fc)",
+        "bound": "mfma", "achieved": fc_tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+        "frac": fc_tflops / MFMA_BF16_PEAK_TFLOPS,
+        "traffic": read_traffic() if (mode == "bfloat16" and cfg.d_model == 1024) else None,
+        "avg_launch_ms": fc_ms, "launches": fc_n,
+        "alg_flop_per_launch": fc_flops,
+    }
+    return res, eng, sd, seqs, lens, words, out
+
+
+def bench_c2(args):
+    from allie_amd import config
+
+    res, eng, sd, seqs, lens, _, _ = run_prefill(
+        args, config.MEDIUM, "bfloat16",
+        "C2 ragged prefill: medium shape 24x1024x16, 256 prefixes, lens U[8,400] seed 2")
+    eng.close()
+    res["cpu_baseline"] = None if args.no_cpu_baseline else cpu_baseline(config.MEDIUM, sd, seqs, args.cpu_budget)
+    return res
+
+
+def bench_c5(args):
+    """2x shape with fp8 e4m3 per-output-channel weights on the C2 batch;
+    quality against the bf16 engine on the same weights."""
+    import torch
+
+    from allie_amd import config
+    from allie_amd.engine import Engine
+
+    cfg = config.LARGE2X
+    res, eng, sd, seqs, lens, words, out = run_prefill(
+        args, cfg, "fp8w", "C5 fp8-weight ablation: 32x1280x20, C2 batch (256 prefixes, lens U[8,400] seed 2)")
+    ref_logits = out.logits.clone()
+    ref_top1 = out.top1.clone()
+    eng.close()
+    del eng
+    torch.cuda.empty_cache()
+    bf = Engine(cfg, sd, mode="bfloat16", device="cuda:0")
+    ob = bf.prefill(words, lens)
+    torch.cuda.synchronize()
+    agree = float((ob.top1 == ref_top1).float().mean().item())
+    err = float((ob.logits - ref_logits).abs().max().item())
+    bf.close()
+    res["config"].update(top1_agreement_vs_bf16=agree, max_abs_logit_err_vs_bf16=err)
+    res["cpu_baseline"] = None
+    return res
+
+
+# ------------------------------------------------------------------------ C3
+def bench_c3(args):
+    import torch
+
+    from allie_amd import capi, config, weights
+    from allie_amd.engine import Engine
+    from allie_amd.tree import TreeExpansion, TreeLayout
+
+    cfg = config.MEDIUM
+    lay = TreeLayout(n_roots=64, prefix_len=200, branching=8, depth=4)
+    eng = Engine(cfg, weights.init_weights(cfg, seed=0), mode="bfloat16", device="cuda:0")
+    tx = TreeExpansion(eng, lay, seed=3)
+    outs = [None] * lay.depth
+
+    def run_tree(probe_levels=()):
+        tx.prefill_roots()
+        times, attn = [], {}
+        for k in range(1, lay.depth + 1):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            p = Probe(capi.PROBE_ATTN, cfg.n_layer) if k in probe_levels else None
+            e0.record()
+            outs[k - 1] = tx.expand_level(k, out=outs[k - 1])
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
+            if p:
+                attn[k] = p.end()
+        return times, attn
+
+    for _ in range(max(args.warmup, 1)):
+        run_tree()
+    assert int(tx.status.item()) == 0, "extend status"
+    level_ms = np.zeros(lay.depth)
+    attn = {}
+    for _ in range(args.steps):
+        t, attn = run_tree(probe_levels=(1, 2))
+        level_ms += np.array(t)
+    level_ms /= args.steps
+    d, L, P = cfg.d_model, cfg.n_layer, lay.prefix_len
+    kv_tok = 2 * d * 2  # bytes of one token's keys + values, one layer
+    roof = {}
+    for k in (1, 2):
+        n = lay.level_size(k)
+        bytes_ = lay.n_roots * P * kv_tok + n * k * kv_tok + n * 2 * d * 2
+        tot, cnt = attn[k]
+        ms = tot / max(cnt, 1)
+        roof[k] = {"avg_launch_ms": ms, "alg_bytes_per_launch": bytes_, "achieved_GBs": bytes_ / (ms * 1e-3) / 1e9}
+    total_ms = float(level_ms.sum())
+    leaves = lay.level_size(lay.depth)
+    flops = sum(2 * cfg.linear_params * lay.level_size(k) + 4 * d * L * lay.level_size(k) * (P + k)
+                for k in range(1, lay.depth + 1))
+    res = base_result(args, leaves / (total_ms / 1000.0), "leaf evals/s", total_ms, "bf16",
+                      "C3 MCTS tree expansion: medium bf16, 64 roots x 200-token prefix (paged, block 16), "
+                      "depth 4, branching 8 (262,144 leaves)",
+                      level_ms=[float(x) for x in level_ms],
+                      node_evals_per_s=lay.n_nodes / (total_ms / 1000.0),
+                      whole_tree_mfma_frac=flops / (total_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+                      roots_prefill_untimed=True)
+    a1 = roof[1]
+    res["roofline"] = {"kernel": "attn_extend_tree_kernel (level 1: 512 nodes over 64 shared prefixes)",
+                       "bound": "hbm", "achieved": a1["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": a1["achieved_GBs"] / HBM_PEAK_GBS, "traffic": None,
+                       "level2": roof[2]}
+    res["cpu_baseline"] = None
+    eng.close()
+    return res
+
+
+# ------------------------------------------------------------------------ C4
+def bench_c4(args):
+    import torch
+
+    from allie_amd import capi, config, weights
+    from allie_amd.batcher import ContinuousBatcher
+    from allie_amd.engine import Engine
+
+    cfg = config.MEDIUM
+    eng = Engine(cfg, weights.init_weights(cfg, seed=0), mode="bfloat16", device="cuda:0")
+    cb = ContinuousBatcher(eng, n_slots=args.slots)
+    for _ in range(args.warmup):
+        cb.step()
+    torch.cuda.synchronize()
+    assert int(cb.status.item()) == 0, "extend status"
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    probed = min(args.steps, 100)  # attention launches are timed in the first 100 steps
+    ctx_probed, ctx_all = 0, 0
+    probe = Probe(capi.PROBE_ATTN, probed * cfg.n_layer)
+    t0 = time.perf_counter()
+    evs[0].record()
+    for i in range(args.steps):
+        keys = int(cb.cur.sum()) + cb.S  # keys read per layer this step (context + the new token)
+        ctx_all += keys
+        ctx_probed += keys if i < probed else 0
+        cb.step()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    att_tot, att_n = probe.end()
+    lat = np.array([evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)])
+    ms = el * 1000.0 / args.steps
+    tok_s = cb.S * args.steps / el
+    d = cfg.d_model
+    att_ms = att_tot / max(att_n, 1)
+    att_bytes = (ctx_probed / probed) * 2 * d * 2 + cb.S * 3 * d * 2  # K,V read + q in, out
+    achieved = att_bytes / (att_ms * 1e-3) / 1e9
+    res = base_result(args, tok_s, "tokens/s", ms, "bf16",
+                      f"C4 continuous-batching self-play decode: medium bf16, {cb.S} slots, prefixes U[1,50], "
+                      "game length Geometric(mean 80) capped 512, greedy argmax, refill on finish",
+                      step_ms_p50=float(np.percentile(lat, 50)), step_ms_p90=float(np.percentile(lat, 90)),
+                      step_ms_p99=float(np.percentile(lat, 99)), mean_context=ctx_all / args.steps / cb.S,
+                      games_started=cb.games_started)
+    res["roofline"] = {"kernel": "attn_extend_wave_kernel (decode attention over the paged cache)",
+                       "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": achieved / HBM_PEAK_GBS, "traffic": None, "avg_launch_ms": att_ms,
+                       "alg_bytes_per_launch": att_bytes}
+    res["cpu_baseline"] = None
+    eng.close()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--config", choices=["c2", "c3", "c4", "c5"], default="c2")
+    ap.add_argument("--slots", type=int, default=1024, help="c4: concurrent games")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -136,78 +372,10 @@ def main():
     if args.calibrate_copy:
         calibrate_copy()
         return
-
-    import torch
-
-    from allie_amd import capi, config, weights
-    from allie_amd.engine import Engine
-
-    cfg = config.MEDIUM
-    sd = weights.init_weights(cfg, seed=0)
-    seqs, lens = c2_batch()
-    T = int(lens.sum())
-    eng = Engine(cfg, sd, mode="bfloat16", device="cuda:0")
-    words = torch.from_numpy(np.concatenate(seqs).view(np.int32)).cuda()
-    out = eng.prefill(words, lens)
-    for _ in range(args.warmup):
-        eng.prefill(words, lens, out=out)
-    torch.cuda.synchronize()
-
-    L = capi.lib()
-    capi.check(L.allie_probe_begin(capi.PROBE_FC, args.steps * cfg.n_layer), "probe")
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        eng.prefill(words, lens, out=out)
-    torch.cuda.synchronize()
-    el = time.perf_counter() - t0
-    tot_ms, n_l = C.c_float(), C.c_int()
-    capi.check(L.allie_probe_end(C.byref(tot_ms), C.byref(n_l)), "probe end")
-
-    ms = el * 1000.0 / args.steps
-    flops = alg_flops(cfg, lens)
-    fc_flops = 2.0 * T * cfg.d_ff * cfg.d_model
-    fc_ms = tot_ms.value / max(n_l.value, 1)
-    fc_tflops = fc_flops / (fc_ms * 1e-3) / 1e12
-    traffic = read_traffic()
-    res = {
-        "metric": "leaf evals/sec @ medium, ragged batch 256; % of MFMA / HBM roofline",
-        "value": 256.0 / (ms / 1000.0),
-        "unit": "leaf evals/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": ms,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded ragged prefixes, random-init GPT-2 weights)",
-        "config": {
-            "workload": "C2 ragged prefill: medium shape 24x1024x16, 256 prefixes, lens U[8,400] seed 2",
-            "n_seq": 256,
-            "n_tokens": T,
-            "tokens_per_s": T / (ms / 1000.0),
-            "alg_tflop_per_step": flops / 1e12,
-            "whole_forward_mfma_frac": flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-            "parallelism": "single GPU",
-        },
-        "roofline": {
-            "kernel": "gemm_mfma_kernel<EPI_GELU,W_BF16> (MLP c_fc)",
-            "bound": "mfma",
-            "achieved": fc_tflops,
-            "peak": MFMA_BF16_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": fc_tflops / MFMA_BF16_PEAK_TFLOPS,
-            "traffic": traffic,
-            "avg_launch_ms": fc_ms,
-            "launches": n_l.value,
-        },
-        "cpu_baseline": None,
-    }
-    eng.close()
-    if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(cfg, sd, seqs, args.cpu_budget)
+    defaults = {"c2": (10, 3), "c3": (3, 1), "c4": (2000, 200), "c5": (10, 3)}[args.config]
+    args.steps = defaults[0] if args.steps is None else args.steps
+    args.warmup = defaults[1] if args.warmup is None else args.warmup
+    res = {"c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.config](args)
     print(json.dumps(res), flush=True)
 
 
