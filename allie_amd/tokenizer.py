@@ -43,18 +43,35 @@ class Game:
     moves_seconds: list[int]
     next_move_seconds: Optional[int] = None
     legal: Optional[list[str]] = field(default=None, repr=False, compare=False)
+    _board: Optional[object] = field(default=None, repr=False, compare=False)
+    _parent: Optional["Game"] = field(default=None, repr=False, compare=False)
 
     @property
     def white_to_move(self) -> bool:
         return len(self.moves) % 2 == 0
 
     @property
-    def legal_moves(self) -> list[str]:
-        if self.legal is not None:
-            return self.legal
-        from . import movegen  # host move generator
+    def board(self):
+        """The position after the game's moves (data.py:51-56), from the
+        host rules of ``allie_amd.movegen``; a child made by ``make_move``
+        extends its parent's cached board by one move."""
+        if self._board is None:
+            from . import movegen
 
-        self.legal = movegen.legal_moves(self.moves)
+            p = self._parent
+            if p is not None and p._board is not None:
+                self._board = p._board.push_uci(self.moves[-1])
+            else:
+                self._board = movegen.board_after(self.moves)
+            self._parent = None
+        return self._board
+
+    @property
+    def legal_moves(self) -> list[str]:
+        """UCI legal moves (data.py:58-61); an explicit ``legal`` list from
+        the caller takes precedence."""
+        if self.legal is None:
+            self.legal = self.board.legal_uci()
         return self.legal
 
     def make_move(self, move: str) -> "Game":
@@ -69,6 +86,7 @@ class Game:
             self.moves + [move],
             self.moves_seconds + [0],
             None,
+            _parent=self,
         )
 
 
