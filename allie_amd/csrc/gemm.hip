@@ -358,23 +358,48 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
     }
     // read back: lane -> row (lane / 8) + 8 it, columns 8 (lane % 8) .. +7
     const int cl = (lane & 7) * 8;
+    if constexpr (EPI == EPI_RESID) {
+      // R += the bf16-rounded value (exact in fp32).  All loads of R for 8
+      // rows are issued before any store: a store may alias the next load, so
+      // interleaving them would expose the memory latency 16 times.
+      float* __restrict__ Rp = a.R;
+#pragma unroll
+      for (int half8 = 0; half8 < 2; ++half8) {
+        uint4 v[8];
+        float4 h0[8], h1[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int ml = (half8 * 8 + u) * 8 + (lane >> 3);
+          const int m = m0 + wm * 128 + ml;
+          v[u] = *reinterpret_cast<const uint4*>(reg + ml * EP + cl);
+          if (m < a.M) {
+            const float4* r = reinterpret_cast<const float4*>(Rp + (int64_t)m * a.ldr + n_base + cl);
+            h0[u] = r[0];
+            h1[u] = r[1];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int ml = (half8 * 8 + u) * 8 + (lane >> 3);
+          const int m = m0 + wm * 128 + ml;
+          if (m >= a.M) continue;
+          float4 x0 = h0[u], x1 = h1[u];
+          x0.x += bf2f(v[u].x & 0xffffu); x0.y += bf2f(v[u].x >> 16);
+          x0.z += bf2f(v[u].y & 0xffffu); x0.w += bf2f(v[u].y >> 16);
+          x1.x += bf2f(v[u].z & 0xffffu); x1.y += bf2f(v[u].z >> 16);
+          x1.z += bf2f(v[u].w & 0xffffu); x1.w += bf2f(v[u].w >> 16);
+          float4* r = reinterpret_cast<float4*>(Rp + (int64_t)m * a.ldr + n_base + cl);
+          r[0] = x0;
+          r[1] = x1;
+        }
+      }
+    } else {
 #pragma unroll 4
-    for (int it = 0; it < 16; ++it) {
-      const int ml = it * 8 + (lane >> 3);
-      const int m = m0 + wm * 128 + ml;
-      const uint4 v = *reinterpret_cast<const uint4*>(reg + ml * EP + cl);
-      if (m >= a.M) continue;
-      if constexpr (EPI == EPI_RESID) {
-        // R += the bf16-rounded value (exact in fp32)
-        float4* r = reinterpret_cast<float4*>(a.R + (int64_t)m * a.ldr + n_base + cl);
-        float4 h0 = r[0], h1 = r[1];
-        h0.x += bf2f(v.x & 0xffffu); h0.y += bf2f(v.x >> 16);
-        h0.z += bf2f(v.y & 0xffffu); h0.w += bf2f(v.y >> 16);
-        h1.x += bf2f(v.z & 0xffffu); h1.y += bf2f(v.z >> 16);
-        h1.z += bf2f(v.w & 0xffffu); h1.w += bf2f(v.w >> 16);
-        r[0] = h0;
-        r[1] = h1;
-      } else {
+      for (int it = 0; it < 16; ++it) {
+        const int ml = it * 8 + (lane >> 3);
+        const int m = m0 + wm * 128 + ml;
+        const uint4 v = *reinterpret_cast<const uint4*>(reg + ml * EP + cl);
+        if (m >= a.M) continue;
         *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(a.C) + (int64_t)m * a.ldc + n_base + cl) = v;
       }
     }
