@@ -12,16 +12,25 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
-// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
-ALLIE_DEV uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16, round to nearest even: gfx950's v_cvt_pk_bf16_f32 converts
+// two values per instruction (NaN stays NaN).
+ALLIE_DEV uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2_t v;
+  v[0] = (__bf16)lo;
+  v[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, v);
 }
+ALLIE_DEV uint32_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 ALLIE_DEV float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
-ALLIE_DEV float round_bf16(float f) { return bf2f(f2bf(f)); }
-ALLIE_DEV uint32_t pack_bf16x2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
+ALLIE_DEV float round_bf16(float f) { return (float)(__bf16)f; }
+// two values rounded to bf16 and widened back (one conversion instruction)
+ALLIE_DEV void round_bf16x2(float& a, float& b) {
+  const uint32_t p = pack_bf16x2(a, b);
+  a = __uint_as_float(p << 16);
+  b = __uint_as_float(p & 0xffff0000u);
+}
 
 // Elements OFF .. OFF+7 of x -> hi = bf16(x), lo = bf16(x - hi): hi + lo
 // carries ~16 mantissa bits of x (for MFMA operands that need more than
@@ -32,9 +41,8 @@ ALLIE_DEV void split_bf16x8(const f32x16_t& x, bf16x8_t& hi, bf16x8_t& lo) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const float x0 = x[OFF + 2 * e], x1 = x[OFF + 2 * e + 1];
-    const uint32_t h0 = f2bf(x0), h1 = f2bf(x1);
-    h[e] = h0 | (h1 << 16);
-    l[e] = pack_bf16x2(x0 - bf2f(h0), x1 - bf2f(h1));
+    h[e] = pack_bf16x2(x0, x1);
+    l[e] = pack_bf16x2(x0 - __uint_as_float(h[e] << 16), x1 - __uint_as_float(h[e] & 0xffff0000u));
   }
   hi = __builtin_bit_cast(bf16x8_t, u32x4_t{h[0], h[1], h[2], h[3]});
   lo = __builtin_bit_cast(bf16x8_t, u32x4_t{l[0], l[1], l[2], l[3]});
@@ -77,8 +85,9 @@ ALLIE_DEV float tanh_fast(float x) {
 // (relative error ~1e-7, far below the bf16 rounding of the result).
 ALLIE_DEV float gelu_tanh_fast(float x) {
   const float k2 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;  // -2 sqrt(2/pi) log2(e)
-  const float u = x + 0.044715f * (x * x * x);
-  const float e = __builtin_amdgcn_exp2f(k2 * u);
+  // k2 u = x (k2 + k2 0.044715 x^2)
+  const float t = x * fmaf(x * x, k2 * 0.044715f, k2);
+  const float e = __builtin_amdgcn_exp2f(t);
   return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 

@@ -195,14 +195,31 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
     }
   };
 
-  f32x16_t acc[FN][FM];
-#pragma unroll
-  for (int i = 0; i < FN; ++i)
-#pragma unroll
-    for (int j = 0; j < FM; ++j) acc[i][j] = f32x16_t{};
-
   const int wm = wave & 1, wn = wave >> 1;
   const int frow = lane & 31, half = lane >> 5;
+  const int n_base = n0 + wn * 64;
+
+  // accumulator element (i, j, q, e) is output (m, n) with
+  // m = m0 + wm 128 + j 32 + frow, n = n_base + i 32 + q 8 + half 4 + e.
+  // bf16 weights: the accumulators start at the bias (fp8 weights scale the
+  // sum first, so their bias is added in the epilogue).
+  f32x16_t acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i) {
+    f32x16_t init{};
+    if (!FP8 && a.bias) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 b = *reinterpret_cast<const float4*>(a.bias + n_base + i * 32 + q * 8 + half * 4);
+        init[q * 4 + 0] = b.x;
+        init[q * 4 + 1] = b.y;
+        init[q * 4 + 2] = b.z;
+        init[q * 4 + 3] = b.w;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acc[i][j] = init;
+  }
 
   // fragments of step `st` of the k-tile in stage s
   auto load_a = [&](int s, int st, bf16x8_t(&xf)[FM]) {
@@ -302,29 +319,19 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
   }
 
   // ---- epilogue ------------------------------------------------------------
-  // accumulator element (i, j, q, e) is output (m, n) with
-  // m = m0 + wm 128 + j 32 + frow, n = n0 + wn 64 + i 32 + q 8 + half 4 + e
-  auto epi_value = [&](float v, float scl, float bias) {
-    v = v * scl + bias;
-    if constexpr (EPI == EPI_GELU) v = gelu_tanh_fast(round_bf16(v));
-    return v;
-  };
-  const int n_base = n0 + wn * 64;
   if constexpr (OUT_F32) {
-    // heads (small M): direct 16-byte stores of fp32 rows
+    // heads (small M): direct 16-byte stores of fp32 rows (bias already in acc)
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int n = n_base + i * 32 + q * 8 + half * 4;
-        const float4 bias = a.bias ? *reinterpret_cast<const float4*>(a.bias + n) : make_float4(0, 0, 0, 0);
 #pragma unroll
         for (int j = 0; j < FM; ++j) {
           const int m = m0 + wm * 128 + j * 32 + frow;
           if (m >= a.M) continue;
           *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.C) + (int64_t)m * a.ldc + n) =
-              make_float4(epi_value(acc[i][j][q * 4 + 0], 1.f, bias.x), epi_value(acc[i][j][q * 4 + 1], 1.f, bias.y),
-                          epi_value(acc[i][j][q * 4 + 2], 1.f, bias.z), epi_value(acc[i][j][q * 4 + 3], 1.f, bias.w));
+              make_float4(acc[i][j][q * 4 + 0], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
         }
       }
     }
@@ -340,18 +347,34 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int nl = i * 32 + q * 8 + half * 4;  // column inside the sub-tile
-        const float4 bias = a.bias ? *reinterpret_cast<const float4*>(a.bias + n_base + nl)
-                                   : make_float4(0, 0, 0, 0);
-        float4 scl = make_float4(1, 1, 1, 1);
-        if constexpr (FP8) scl = *reinterpret_cast<const float4*>(a.scale + n_base + nl);
+        float4 bias = make_float4(0, 0, 0, 0), scl = make_float4(1, 1, 1, 1);
+        if constexpr (FP8) {
+          if (a.bias) bias = *reinterpret_cast<const float4*>(a.bias + n_base + nl);
+          scl = *reinterpret_cast<const float4*>(a.scale + n_base + nl);
+        }
 #pragma unroll
         for (int j = 0; j < FM; ++j) {
           const int ml = j * 32 + frow;
+          float v0 = acc[i][j][q * 4 + 0], v1 = acc[i][j][q * 4 + 1];
+          float v2 = acc[i][j][q * 4 + 2], v3 = acc[i][j][q * 4 + 3];
+          if constexpr (FP8) {
+            v0 = v0 * scl.x + bias.x;
+            v1 = v1 * scl.y + bias.y;
+            v2 = v2 * scl.z + bias.z;
+            v3 = v3 * scl.w + bias.w;
+          }
+          if constexpr (EPI == EPI_GELU) {
+            // gelu_new of the bf16 addmm result
+            round_bf16x2(v0, v1);
+            round_bf16x2(v2, v3);
+            v0 = gelu_tanh_fast(v0);
+            v1 = gelu_tanh_fast(v1);
+            v2 = gelu_tanh_fast(v2);
+            v3 = gelu_tanh_fast(v3);
+          }
           uint2 p;
-          p.x = pack_bf16x2(epi_value(acc[i][j][q * 4 + 0], scl.x, bias.x),
-                            epi_value(acc[i][j][q * 4 + 1], scl.y, bias.y));
-          p.y = pack_bf16x2(epi_value(acc[i][j][q * 4 + 2], scl.z, bias.z),
-                            epi_value(acc[i][j][q * 4 + 3], scl.w, bias.w));
+          p.x = pack_bf16x2(v0, v1);
+          p.y = pack_bf16x2(v2, v3);
           *reinterpret_cast<uint2*>(reg + ml * EP + nl) = p;
         }
       }

@@ -161,6 +161,40 @@ def test_gemm_bf16_epilogues(M, N, K, cuda):
     assert ((R - (R0 + acc)).abs() <= acc.abs() * 2 ** -8 + 1e-5).all()
 
 
+def test_gemm_epilogue_rounds_to_nearest_even(cuda):
+    """The bf16 epilogues round fp32 sums to nearest even, bit for bit: A's
+    row m carries a two-way bf16 split of x_m (hi + lo == x_m exactly, x_m
+    having 16 significant bits) against weight ones, so the fp32 sum is
+    exactly x_m in any summation order, and the stored bf16 must equal
+    torch's RNE conversion of x_m; half of the x_m sit exactly halfway
+    between two bf16 values."""
+    rng = np.random.default_rng(11)
+    M, N, K = 1000, 128, 32
+    bits = rng.integers(0x3A800000, 0x44800000, M, dtype=np.int64) & ~0xFF  # ~1e-3 .. 1e3
+    bits[::2] = (bits[::2] & ~0xFFFF) | 0x8000  # ties
+    sign = np.where(rng.random(M) < 0.5, np.int64(1) << 31, 0)
+    x = torch.from_numpy((bits | sign).astype(np.uint32).view(np.float32).copy())
+    hi = rb(x)
+    lo = x - hi
+    assert torch.equal(rb(lo), lo) and torch.equal(hi + lo, x) and not torch.equal(hi, x)
+    A = torch.zeros(M, K)
+    A[:, 0], A[:, 1] = hi, lo
+    A = A.to(torch.bfloat16).to(cuda)
+    Wt = torch.zeros(N, K)
+    Wt[:, :2] = 1.0
+    Wt = Wt.to(torch.bfloat16).to(cuda)
+    want = x.to(torch.bfloat16)[:, None].expand(M, N)
+    zero_bias = torch.zeros(N, device=cuda)
+    for b in (None, zero_bias):
+        C_ = _gemm(A, Wt, b, capi.EPI_STORE, capi.WT_BF16).cpu()
+        assert torch.equal(C_.view(torch.int16), want.contiguous().view(torch.int16))
+        R = torch.zeros(M, N, device=cuda)
+        _gemm(A, Wt, b, capi.EPI_RESID, capi.WT_BF16, R=R)
+        assert torch.equal(R.cpu(), want.float())
+        C32 = _gemm(A, Wt, b, capi.EPI_STORE, capi.WT_BF16, out_f32=True).cpu()
+        assert torch.equal(C32, x[:, None].expand(M, N))
+
+
 @pytest.mark.parametrize("M,N,K", [(300, 768, 256), (1000, 3072, 1024)])
 def test_gemm_fp8_weights(M, N, K, cuda):
     g = torch.Generator(device="cpu").manual_seed(N + K)
