@@ -134,9 +134,11 @@ def _gemm(A, Wt, bias, epi, wtype, out_f32=False, R=None, scale=None):
 
 
 SHAPES = [(1, 256, 64), (300, 768, 256), (777, 1024, 1024), (1000, 3072, 1024), (513, 1024, 4096), (64, 4096, 1024)]
+# large grids: ragged last m-tile, several rounds of blocks per CU, K of 4 k-tiles
+LARGE_SHAPES = [(4100, 4096, 256), (16400, 1024, 512), (8192, 3072, 128)]
 
 
-@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("M,N,K", SHAPES + LARGE_SHAPES)
 def test_gemm_bf16_epilogues(M, N, K, cuda):
     g = torch.Generator(device="cpu").manual_seed(M * 7 + N + K)
     A = torch.randn(M, K, generator=g).to(torch.bfloat16).to(cuda)
@@ -161,7 +163,8 @@ def test_gemm_bf16_epilogues(M, N, K, cuda):
     assert ((R - (R0 + acc)).abs() <= acc.abs() * 2 ** -8 + 1e-5).all()
 
 
-def test_gemm_epilogue_rounds_to_nearest_even(cuda):
+@pytest.mark.parametrize("M,N", [(1000, 128), (4100, 4096)])
+def test_gemm_epilogue_rounds_to_nearest_even(M, N, cuda):
     """The bf16 epilogues round fp32 sums to nearest even, bit for bit: A's
     row m carries a two-way bf16 split of x_m (hi + lo == x_m exactly, x_m
     having 16 significant bits) against weight ones, so the fp32 sum is
@@ -169,7 +172,7 @@ def test_gemm_epilogue_rounds_to_nearest_even(cuda):
     torch's RNE conversion of x_m; half of the x_m sit exactly halfway
     between two bf16 values."""
     rng = np.random.default_rng(11)
-    M, N, K = 1000, 128, 32
+    K = 32
     bits = rng.integers(0x3A800000, 0x44800000, M, dtype=np.int64) & ~0xFF  # ~1e-3 .. 1e3
     bits[::2] = (bits[::2] & ~0xFFFF) | 0x8000  # ties
     sign = np.where(rng.random(M) < 0.5, np.int64(1) << 31, 0)
@@ -195,7 +198,7 @@ def test_gemm_epilogue_rounds_to_nearest_even(cuda):
         assert torch.equal(C32, x[:, None].expand(M, N))
 
 
-@pytest.mark.parametrize("M,N,K", [(300, 768, 256), (1000, 3072, 1024)])
+@pytest.mark.parametrize("M,N,K", [(300, 768, 256), (1000, 3072, 1024), (4100, 4096, 256)])
 def test_gemm_fp8_weights(M, N, K, cuda):
     g = torch.Generator(device="cpu").manual_seed(N + K)
     A = torch.randn(M, K, generator=g).to(torch.bfloat16).to(cuda)
