@@ -5,8 +5,8 @@ full forward of the whole game at batch 1 for every appended move
 (src/evaluation/decode.py:199-226, argmax at decode.py:112).  Here S slots
 each hold a game; one step appends the greedy move of every slot with a
 single ``Engine.extend`` over cached keys and values, finished games are
-evicted and their slots refilled (prefill of the new game's prefix into the
-slot's blocks), with no host synchronisation in the loop: the host knows
+evicted and their slots refilled (the new game's prefix joins the next
+step's forward), with no host synchronisation in the loop: the host knows
 every game's length in advance, and the moves themselves stay on the GPU.
 
 KV layout: slot s owns the pool blocks [s * B, (s + 1) * B) with
@@ -83,7 +83,19 @@ class PinnedUploader:
 
 
 class ContinuousBatcher:
-    """``record=True`` (tests) keeps each slot's game on the host and every
+    """S slots of self-play games over the paged KV cache.
+
+    One ``step`` is one ``Engine.extend`` over every slot: a running game
+    feeds its last greedy move (a one-token group over the slot's cached
+    keys), a game started since the previous step feeds its whole prefix (a
+    group whose prefix is the game's own P positions, written by the same
+    forward; token t sees positions 0..t), so new games ride in the same
+    forward as the decode steps instead of a separate prefill.  Finished games are evicted at the end of a step and their slots
+    drawn anew for the next one.  All integer metadata is known on the host
+    (lengths, positions, pool slots); only the moves live on the GPU, so the
+    loop never synchronises.
+
+    ``record=True`` (tests) keeps each slot's game on the host and every
     (game so far, greedy move predicted for it) pair in ``checks``; it reads
     the moves back every step, so it synchronises the stream."""
 
@@ -100,61 +112,85 @@ class ContinuousBatcher:
         self.table = (torch.arange(n_slots, dtype=torch.int32, device=dev)[:, None] * self.bps
                       + torch.arange(self.bps, dtype=torch.int32, device=dev)[None, :]).contiguous()
         self.queue = queue or GameQueue()
-        self.up = PinnedUploader(dev, capacity=max(4096, n_slots * 64))
-        # per-slot state: host knows lengths, the device holds the moves
+        self.up = PinnedUploader(dev, capacity=max(8192, n_slots * 512))
         self.cur = np.zeros(n_slots, np.int32)    # tokens cached per slot
         self.total = np.zeros(n_slots, np.int32)  # game length to reach
-        self.cur_dev = torch.zeros(n_slots, dtype=torch.int32, device=dev)
         self.next_tok = torch.zeros(n_slots, dtype=torch.int32, device=dev)
-        self.ones = torch.ones(n_slots, dtype=torch.int32, device=dev)
+        self.ones = torch.ones(n_slots * 64, dtype=torch.int32, device=dev)
         self.status = torch.zeros(1, dtype=torch.int32, device=dev)
         self.games_started = 0
-        self.tokens = 0
+        self.tokens = 0        # moves appended
+        self.keys_read = 0     # keys attended per layer, summed over steps
+        self.fed = 0           # tokens fed (moves and new games' prefixes)
         self.record = record
         self.games = [[] for _ in range(n_slots)]
         self.checks = []  # (game so far, predicted next move) when recording
-        self.refill(np.arange(n_slots))
+        self.pending = {}  # slot -> (prefix ids, total length) to start next step
+        self._draw(np.arange(n_slots))
 
-    def refill(self, slots: np.ndarray) -> None:
-        """Start new games in `slots`: prefill their prefixes into the slots'
-        blocks; the prefill's greedy move is the first move to append."""
+    def _draw(self, slots: np.ndarray) -> None:
         if len(slots) == 0:
             return
-        torch = self.torch
         prefixes, P, total = self.queue.draw(len(slots))
-        words = self.up(np.concatenate(prefixes))
-        idx = self.up(slots.astype(np.int32)).long()
-        out = self.eng.prefill(words, P, kv_pool=self.pool, kv_block_table=self.table[idx].contiguous(),
-                               want_logits=False)
-        self.next_tok.index_copy_(0, idx, out.top1)
-        self.cur_dev.index_copy_(0, idx, self.up(P))
-        self.cur[slots] = P
-        self.total[slots] = total
+        for k, s in enumerate(slots):
+            self.pending[int(s)] = (prefixes[k], int(total[k]))
         self.games_started += len(slots)
-        if self.record:
-            top = out.top1.cpu().numpy()
-            for k, s in enumerate(slots):
-                self.games[s] = [int(x) for x in prefixes[k]]
-                self.checks.append((list(self.games[s]), int(top[k])))
 
     def step(self) -> int:
-        """Append one greedy move to every slot; evict and refill finished
-        games.  Returns the number of moves appended."""
+        """Append one greedy move to every running game and start the pending
+        ones; evict finished games.  Returns the number of moves appended."""
         torch = self.torch
-        cur = self.cur_dev
-        fed = self.next_tok.cpu().numpy() if self.record else None
-        slot = torch.gather(self.table, 1, (cur // KV_BLOCK).long()[:, None])[:, 0] * KV_BLOCK + cur % KV_BLOCK
-        out = self.eng.extend(self.next_tok, cur, [1] * self.S, cur, self.table, slot[:, None].contiguous(),
-                              self.ones, self.pool, want_logits=False, status=self.status)
+        pend = sorted(self.pending)
+        is_pend = np.zeros(self.S, bool)
+        is_pend[pend] = True
+        R = np.nonzero(~is_pend)[0].astype(np.int32)  # running slots, one token each
+        nR = len(R)
+        pre = [self.pending[s][0] for s in pend]
+        Ps = np.array([len(p) for p in pre], np.int32)
+        nP = int(Ps.sum())
+        n = nR + nP
+        G = nR + len(pend)
+        slot_stride = self.bps * KV_BLOCK  # pool slots per game slot
+        # host metadata: one pinned upload, sliced on the device
+        pos_p = np.concatenate([np.arange(P, dtype=np.int32) for P in Ps]) if pend else np.zeros(0, np.int32)
+        pos = np.concatenate([self.cur[R], pos_p])
+        prefix_len = np.concatenate([self.cur[R], Ps])
+        gslot = np.concatenate([R, np.array(pend, np.int32)])
+        # each token's only extra is its own pool slot (its key's position)
+        own = np.concatenate([R, np.repeat(np.array(pend, np.int32), Ps)]) * slot_stride + pos
+        ids_p = np.concatenate(pre).astype(np.int32) if pend else np.zeros(0, np.int32)
+        meta = self.up(np.concatenate([pos, prefix_len, gslot, own, ids_p]))
+        o = np.cumsum([0, n, G, G, n, nP])
+        pos_t, pl_t, gs_t, own_t, idsp_t = (meta[o[i]:o[i + 1]] for i in range(5))
+        gs_l = gs_t.long()
+        ids = torch.cat([self.next_tok.index_select(0, gs_l[:nR]), idsp_t])
+        fed = ids[:nR].cpu().numpy() if self.record else None
+        out = self.eng.extend(ids, pos_t, [1] * nR + Ps.tolist(), pl_t, self.table.index_select(0, gs_l),
+                              own_t[:, None], self.ones[:n] if n <= len(self.ones) else torch.ones(
+                                  n, dtype=torch.int32, device=meta.device),
+                              self.pool, want_logits=False, status=self.status)
+        # outputs: running games' next moves, new games' first moves (last prefix token)
+        last = np.concatenate([np.arange(nR), nR + np.cumsum(Ps) - 1]).astype(np.int32) if pend else None
+        if pend:
+            last_t = self.up(last).long()
+            self.next_tok.index_copy_(0, gs_l, out.top1.index_select(0, last_t))
+        else:
+            self.next_tok.index_copy_(0, gs_l, out.top1)
         if self.record:
             top = out.top1.cpu().numpy()
-            for s in range(self.S):
-                self.games[s].append(int(fed[s]))
-                self.checks.append((list(self.games[s]), int(top[s])))
-        self.next_tok.copy_(out.top1)
-        self.cur_dev += 1
-        self.cur += 1
-        self.tokens += self.S
-        done = np.nonzero(self.cur >= self.total)[0]
-        self.refill(done)
-        return self.S
+            for k, s in enumerate(R):
+                self.games[s].append(int(fed[k]))
+                self.checks.append((list(self.games[s]), int(top[k])))
+            for k, s in enumerate(pend):
+                self.games[s] = [int(x) for x in pre[k]]
+                self.checks.append((list(self.games[s]), int(top[last[nR + k]])))
+        self.keys_read += int(self.cur[R].sum()) + nR + int((Ps * (Ps + 1) // 2).sum())
+        self.cur[R] += 1
+        for k, s in enumerate(pend):
+            self.cur[s] = Ps[k]
+            self.total[s] = self.pending[s][1]
+        self.pending = {}
+        self.tokens += nR
+        self.fed += n
+        self._draw(np.nonzero(self.cur >= self.total)[0])
+        return nR

@@ -79,11 +79,11 @@ __global__ __launch_bounds__(PREP_THREADS) void extend_prepare_kernel(ExtendPrep
 // Tile list of the tree kernel: (g << 8) | t for t < ceil(size_g / 64), groups
 // in order.  One workgroup; exclusive scan of the per-group tile counts.
 __global__ __launch_bounds__(PREP_THREADS) void extend_tiles_kernel(const int32_t* __restrict__ group_start,
-                                                                    int G, int32_t* __restrict__ tiles) {
+                                                                    int g0, int G, int32_t* __restrict__ tiles) {
   __shared__ int sh[PREP_THREADS / 64 + 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int carry = 0;
-  for (int base = 0; base < G; base += PREP_THREADS) {
+  for (int base = g0; base < G; base += PREP_THREADS) {
     const int g = base + threadIdx.x;
     const int nt = g < G ? (group_start[g + 1] - group_start[g] + QT - 1) / QT : 0;
     int x = nt;  // inclusive wave scan
@@ -189,7 +189,9 @@ __global__ __launch_bounds__(256) void attn_extend_wave_kernel(ExtendAttnArgs a)
     m_run = m_new;
   };
 
-  const int P = a.prefix_len[g];
+  // visible prefix: positions below both the group's prefix length and the
+  // token's own position (a new game's prefix tokens see only earlier ones)
+  const int P = min(a.prefix_len[g], a.pos[i]);
   const int nb = (P + KV_BLOCK - 1) / KV_BLOCK;
   for (int b = 0; b < nb && b < a.max_blocks; ++b) {
     const int blk = a.prefix_blocks[(int64_t)g * a.max_blocks + b];
@@ -263,7 +265,10 @@ __global__ __launch_bounds__(128) void attn_extend_tree_kernel(ExtendAttnArgs a)
   f32x16_t o[2] = {f32x16_t{}, f32x16_t{}};
 
   // ---- phase 1: the group's prefix, 64 keys (4 pool blocks) per LDS tile ----
+  // query qi sees prefix positions below lim (its own position when that is
+  // inside the prefix: the tokens of a new game's prefix)
   const int P = a.prefix_len[g];
+  const int lim = q_ok ? min(P, a.pos[qi]) : P;
   const int32_t* btab = a.prefix_blocks + (int64_t)g * a.max_blocks;
   for (int k0 = 0; k0 < P; k0 += KT) {
     __syncthreads();
@@ -300,7 +305,8 @@ __global__ __launch_bounds__(128) void attn_extend_tree_kernel(ExtendAttnArgs a)
         st[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], st[b], 0, 0, 0);
       }
     }
-    // keys past the prefix (or in a skipped block) are masked
+    // keys past the prefix, at or past the query's position, or in a skipped
+    // block are masked
     float mx = -INFINITY;
 #pragma unroll
     for (int b = 0; b < 2; ++b)
@@ -310,7 +316,7 @@ __global__ __launch_bounds__(128) void attn_extend_tree_kernel(ExtendAttnArgs a)
         const int bi = p / KV_BLOCK;
         const int blk = (p < P && bi < a.max_blocks) ? btab[bi] : -1;
         float v = st[b][r] * sl2;
-        if (blk < 0 || blk >= a.pool_blocks) v = -INFINITY;
+        if (blk < 0 || blk >= a.pool_blocks || p >= lim) v = -INFINITY;
         st[b][r] = v;
         mx = fmaxf(mx, v);
       }
@@ -421,9 +427,11 @@ hipError_t launch_extend_prepare(const ExtendPrepArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-hipError_t launch_extend_tiles(const int32_t* group_start, int n_groups, int32_t* tiles, hipStream_t st) {
-  if (n_groups == 0) return hipSuccess;
-  hipLaunchKernelGGL(extend_tiles_kernel, dim3(1), dim3(PREP_THREADS), 0, st, group_start, n_groups, tiles);
+hipError_t launch_extend_tiles(const int32_t* group_start, int first_group, int n_groups, int32_t* tiles,
+                               hipStream_t st) {
+  if (first_group >= n_groups) return hipSuccess;
+  hipLaunchKernelGGL(extend_tiles_kernel, dim3(1), dim3(PREP_THREADS), 0, st, group_start, first_group, n_groups,
+                     tiles);
   return hipGetLastError();
 }
 

@@ -744,15 +744,17 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   if (group_start_host[0] != 0 || group_start_host[n_groups] != n_tok)
     return fail(ALLIE_ERR_ARG, "group_start must run from 0 to n_tok");
   if (n_groups > (1 << 23)) return fail(ALLIE_ERR_ARG, "too many groups");
-  int64_t n_tiles = 0;
   int max_group = 0;
+  int n1 = 0;  // leading groups of one token each (decode steps)
   for (int g = 0; g < n_groups; ++g) {
     const int sz = group_start_host[g + 1] - group_start_host[g];
     if (sz <= 0) return fail(ALLIE_ERR_ARG, "group %d is empty", g);
     if (sz > 64 * 256) return fail(ALLIE_ERR_ARG, "group %d has %d tokens (max 16384)", g, sz);
     max_group = sz > max_group ? sz : max_group;
-    n_tiles += (sz + 63) / 64;
+    if (n1 == g && sz == 1) n1 = g + 1;
   }
+  int64_t n_tiles = 0;  // 64-query tiles of the groups after the leading ones
+  for (int g = n1; g < n_groups; ++g) n_tiles += (group_start_host[g + 1] - group_start_host[g] + 63) / 64;
   ExtendWS w = layout_extend(m, n_tok, n_groups, (char*)workspace);
   if (workspace_bytes < w.total)
     return fail(ALLIE_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, w.total);
@@ -760,9 +762,11 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   const int act = m->act_bf16;
   if ((rc = upload_i32(m, w.group_start, group_start_host, (size_t)n_groups + 1, st))) return rc;
   // the tree kernel shares a group's prefix across a 64-query tile; groups of
-  // one token (decode) stream it with one wave per query
+  // one token (decode) stream it with one wave per query.  A batch that mixes
+  // them (decode steps plus new games' prefixes) puts the one-token groups
+  // first: those n1 tokens go to the wave kernel, the rest to the tree kernel.
   const bool tree = act && max_group > 1;
-  if (tree) HIP_TRY(launch_extend_tiles(w.group_start, n_groups, w.tiles, st));
+  if (tree) HIP_TRY(launch_extend_tiles(w.group_start, n1, n_groups, w.tiles, st));
 
   ExtendPrepArgs pa{};
   pa.n = n_tok;
@@ -801,6 +805,7 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
 
   ExtendAttnArgs xa{};
   xa.qkv = w.qkv;
+  xa.pos = pos;
   xa.n = n_tok;
   xa.n_head = m->H;
   xa.group_start = w.group_start;
@@ -825,7 +830,16 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
                   [&](int layer) -> int {
                     xa.layer = layer;
                     HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, true, st));
-                    HIP_TRY(tree ? launch_attn_extend_tree(xa, st) : launch_attn_extend_wave(xa, st));
+                    if (tree) {
+                      if (n1 > 0) {
+                        ExtendAttnArgs wa = xa;
+                        wa.n = n1;
+                        HIP_TRY(launch_attn_extend_wave(wa, st));
+                      }
+                      HIP_TRY(launch_attn_extend_tree(xa, st));
+                    } else {
+                      HIP_TRY(launch_attn_extend_wave(xa, st));
+                    }
                     HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, false, st));
                     return ALLIE_OK;
                   },

@@ -126,6 +126,7 @@ hipError_t launch_kv_write(const KVWriteArgs& a, hipStream_t st);
 // and slots outside the pool are skipped (and flagged by extend_prepare).
 struct ExtendAttnArgs {
   const void* qkv;             // [n][3d] new tokens (q | k | v)
+  const int32_t* pos;          // [n] token positions: prefix keys at or past pos[i] are not visible
   int n, n_head;
   const int32_t* group_start;  // [G + 1]
   int n_groups;
@@ -147,8 +148,10 @@ struct ExtendAttnArgs {
 hipError_t launch_attn_extend_wave(const ExtendAttnArgs& a, hipStream_t st);
 // MFMA tiles of 64 queries sharing a group's prefix (bf16); needs tiles
 hipError_t launch_attn_extend_tree(const ExtendAttnArgs& a, hipStream_t st);
-// tiles[] = (g << 8) | t for every 64-query tile t of every group g, in order
-hipError_t launch_extend_tiles(const int32_t* group_start, int n_groups, int32_t* tiles, hipStream_t st);
+// tiles[] = (g << 8) | t for every 64-query tile t of every group g in
+// [first_group, n_groups), in order
+hipError_t launch_extend_tiles(const int32_t* group_start, int first_group, int n_groups, int32_t* tiles,
+                               hipStream_t st);
 
 // Validates an extend batch and derives each token's own pool slot (the last
 // of its extras).  status bits: 1 n_extra outside [1, max_extra], 2 a block id

@@ -318,33 +318,38 @@ def bench_c4(args):
     assert int(cb.status.item()) == 0, "extend status"
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     probed = min(args.steps, 100)  # attention launches are timed in the first 100 steps
-    ctx_probed, ctx_all = 0, 0
     probe = Probe(capi.PROBE_ATTN, probed * cfg.n_layer)
+    tok0, keys0, fed0 = cb.tokens, cb.keys_read, 0
+    keys_probed = fed_probed = 0
     t0 = time.perf_counter()
     evs[0].record()
     for i in range(args.steps):
-        keys = int(cb.cur.sum()) + cb.S  # keys read per layer this step (context + the new token)
-        ctx_all += keys
-        ctx_probed += keys if i < probed else 0
+        k_before, f_before = cb.keys_read, cb.fed
         cb.step()
+        if i < probed:
+            keys_probed += cb.keys_read - k_before
+            fed_probed += cb.fed - f_before
         evs[i + 1].record()
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     att_tot, att_n = probe.end()
     lat = np.array([evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)])
     ms = el * 1000.0 / args.steps
-    tok_s = cb.S * args.steps / el
+    appended = cb.tokens - tok0
+    tok_s = appended / el
     d = cfg.d_model
     att_ms = att_tot / max(att_n, 1)
-    att_bytes = (ctx_probed / probed) * 2 * d * 2 + cb.S * 3 * d * 2  # K,V read + q in, out
+    # per attention launch (one layer): keys and values read, queries in, outputs out
+    att_bytes = (keys_probed / probed) * 2 * d * 2 + (fed_probed / probed) * 3 * d * 2
     achieved = att_bytes / (att_ms * 1e-3) / 1e9
     res = base_result(args, tok_s, "tokens/s", ms, "bf16",
                       f"C4 continuous-batching self-play decode: medium bf16, {cb.S} slots, prefixes U[1,50], "
                       "game length Geometric(mean 80) capped 512, greedy argmax, refill on finish",
                       step_ms_p50=float(np.percentile(lat, 50)), step_ms_p90=float(np.percentile(lat, 90)),
-                      step_ms_p99=float(np.percentile(lat, 99)), mean_context=ctx_all / args.steps / cb.S,
-                      games_started=cb.games_started)
-    res["roofline"] = {"kernel": "attn_extend_wave_kernel (decode attention over the paged cache)",
+                      step_ms_p99=float(np.percentile(lat, 99)),
+                      mean_keys_per_step=(cb.keys_read - keys0) / args.steps,
+                      moves_appended=appended, games_started=cb.games_started)
+    res["roofline"] = {"kernel": "extend attention (decode steps and new games' prefixes over the paged cache)",
                        "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": achieved / HBM_PEAK_GBS, "traffic": None, "avg_launch_ms": att_ms,
                        "alg_bytes_per_launch": att_bytes}

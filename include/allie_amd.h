@@ -161,8 +161,10 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
  * Tokens come in n_groups contiguous groups: group g is tokens
  * [group_start_host[g], group_start_host[g+1]) (HOST array, read during the
  * call).  Token i of group g attends
- *   1. the group's shared prefix, positions 0 .. prefix_len[g]-1, stored in
- *      the pool blocks prefix_blocks[g][0 .. ceil(prefix_len[g]/16)-1], then
+ *   1. the group's shared prefix, positions 0 .. min(prefix_len[g], pos[i])-1,
+ *      stored in the pool blocks prefix_blocks[g][0 .. ceil(prefix_len[g]/16)-1]
+ *      (a token placed inside its group's prefix sees only earlier positions),
+ *      then
  *   2. its own keys: pool slots extra_slot[i][0 .. n_extra[i]-1] (a search
  *      node's ancestors in root-to-leaf order, then the node itself).
  * Every layer's key/value of token i is written to pool slot
@@ -173,7 +175,13 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
  * status (device int32[1], optional) is written with 1 a token's n_extra
  * outside [1, max_extra], 2 a block id or slot outside the pool, 4 a position
  * outside the model's positions; keys in bad blocks are skipped, never read.
- * Groups may hold at most 16384 tokens. */
+ * Groups may hold at most 16384 tokens.  A new game's whole prefix of P
+ * tokens is one group with prefix_len P over the game's own blocks, token t
+ * at pos t with its own slot (position t) as its only extra: every layer
+ * writes the P keys before attention, and token t sees positions 0..t.  A
+ * batch may mix such groups with decode steps; one-token groups placed first
+ * are streamed by the decode kernel, the rest share their group's keys
+ * across query tiles. */
 size_t allie_extend_workspace_bytes(const allie_model* m, int n_tok, int n_groups);
 int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_tok,
                  const int32_t* group_start_host, int n_groups, const int32_t* prefix_len,

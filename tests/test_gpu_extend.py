@@ -117,6 +117,73 @@ def test_tree_levels_match_full_recompute(tiny, mode, tol, cuda):
     eng.close()
 
 
+@pytest.mark.parametrize("mode,tol", [("float32", 1e-4), ("bfloat16", 2e-2)])
+def test_mixed_batch_matches_full_recompute(tiny, mode, tol, cuda):
+    """One extend holding decode steps (one-token groups first), new games'
+    whole prefixes and three children sharing a cached game as prefix: the
+    batch a continuous batcher runs when games start between decode steps.
+    A new game's token t attends tokens 0..t, given either as its extras
+    (prefix_len 0; 1 and 70 tokens, the latter over two query tiles) or as
+    the group's own prefix limited by the token's position (prefix_len 45,
+    one extra: its own slot)."""
+    cfg, sd = tiny
+    rng = np.random.default_rng(13)
+    B = 6
+    lens = rng.integers(1, 60, B).astype(np.int32)
+    seqs = [list(rng.integers(0, 1968, n)) for n in lens]
+    eng = Engine(cfg, sd, mode=mode)
+    n_games = B + 3
+    pool = eng.new_kv_pool(n_games * BPG + 1)
+    table = torch.tensor([[g * BPG + j for j in range(BPG)] for g in range(n_games)], dtype=torch.int32,
+                         device=cuda)
+    eng.prefill(np.concatenate([np.asarray(s, np.uint32) for s in seqs]), lens, kv_pool=pool,
+                kv_block_table=table[:B].contiguous())
+    oracle = RefModel(cfg, sd, mode=mode)
+    status = torch.zeros(1, dtype=torch.int32, device=cuda)
+    new_pre = [list(rng.integers(0, 1968, 1)), list(rng.integers(0, 1968, 70))]
+    causal_pre = list(rng.integers(0, 1968, 45))
+    kid_ids = rng.integers(0, 1968, 3)
+    dec = rng.integers(0, 1968, B)
+    ids, pos, sizes, plen, pblk, extra_rows, n_extra, paths = [], [], [], [], [], [], [], []
+    ME = 70
+    for b in range(B):  # decode steps
+        p = len(seqs[b])
+        ids.append(dec[b]); pos.append(p); sizes.append(1); plen.append(p); pblk.append(b)
+        extra_rows.append([b * BPG * 16 + p]); n_extra.append(1)
+        paths.append(seqs[b] + [int(dec[b])])
+    for k, pre in enumerate(new_pre):  # new games, own blocks B + k
+        g = B + k
+        sizes.append(len(pre)); plen.append(0); pblk.append(g)
+        for t, tok in enumerate(pre):
+            ids.append(tok); pos.append(t)
+            extra_rows.append([g * BPG * 16 + e for e in range(t + 1)]); n_extra.append(t + 1)
+            paths.append([int(x) for x in pre[: t + 1]])
+    g = B + 2  # new game over its own prefix positions
+    sizes.append(len(causal_pre)); plen.append(len(causal_pre)); pblk.append(g)
+    for t, tok in enumerate(causal_pre):
+        ids.append(tok); pos.append(t)
+        extra_rows.append([g * BPG * 16 + t]); n_extra.append(1)
+        paths.append([int(x) for x in causal_pre[: t + 1]])
+    kid_slot0 = n_games * BPG * 16  # children's slots: the last block
+    sizes.append(3); plen.append(len(seqs[0])); pblk.append(0)
+    for c in range(3):  # children of game 0 (shared cached prefix)
+        ids.append(kid_ids[c]); pos.append(len(seqs[0]))
+        extra_rows.append([kid_slot0 + c]); n_extra.append(1)
+        paths.append(seqs[0] + [int(kid_ids[c])])
+    extra = np.full((len(ids), ME), -1, np.int32)
+    for i, r in enumerate(extra_rows):
+        extra[i, : len(r)] = r
+    # the decode tokens write their keys into the games' next positions, which
+    # the children do not read (they attend the cached prefix and themselves)
+    out = eng.extend(np.array(ids), np.array(pos, np.int32), sizes, np.array(plen, np.int32),
+                     table.index_select(0, torch.tensor(pblk, device=cuda)), extra,
+                     np.array(n_extra, np.int32), pool, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    check(out, oracle.forward_last([np.asarray(p, np.int64) for p in paths]), tol, f"{mode} mixed batch")
+    eng.close()
+
+
 def test_extend_status_flags(tiny, cuda):
     """Bad slots, counts and positions are flagged and never dereferenced."""
     cfg, sd = tiny

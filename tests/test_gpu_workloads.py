@@ -53,9 +53,14 @@ def test_tree_expansion_matches_recompute(tiny, mode, tol, cuda):
     eng.close()
 
 
-def test_continuous_batching_greedy_moves(tiny, cuda):
+@pytest.mark.parametrize("mode,margin", [("float32", 1e-4), ("bfloat16", 0.1)])
+def test_continuous_batching_greedy_moves(tiny, mode, margin, cuda):
+    """Every recorded (game so far, greedy move) pair against the oracle's
+    full recompute of that game: new games' prefixes ride in the same extend
+    as the running games' decode steps (in bf16 that batch mixes the decode
+    kernel and the tiled kernel)."""
     cfg, sd = tiny
-    eng = Engine(cfg, sd, mode="float32")
+    eng = Engine(cfg, sd, mode=mode)
     q = GameQueue(seed=4, mean_len=12, cap=64, prefix_lo=1, prefix_hi=9)
     cb = ContinuousBatcher(eng, n_slots=5, queue=q, record=True)
     for _ in range(40):
@@ -66,9 +71,9 @@ def test_continuous_batching_greedy_moves(tiny, cuda):
     seqs = [np.asarray(g, np.int64) for g, _ in cb.checks]
     pred = np.array([p for _, p in cb.checks])
     assert max(len(g) for g in seqs) <= 64
-    ref = RefModel(cfg, sd, mode="float32").forward_last(seqs)
+    ref = RefModel(cfg, sd, mode=mode).forward_last(seqs)
     ps = policy_summary(ref["logits"])
-    need = ps["margin"] > 1e-4
-    assert need.mean() > 0.9
+    need = ps["margin"] > margin
+    assert need.mean() > 0.5
     assert (pred[need] == ps["top1"][need]).all(), np.nonzero(pred != ps["top1"])
     eng.close()
