@@ -73,6 +73,10 @@ _SIGS = [
     ("allie_gemm", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
       C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p]),
+    ("allie_gemm_splitk", C.c_int,
+     [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
+      C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_size_t, C.c_void_p]),
+    ("allie_gemm_split_factor", C.c_int, [C.c_int, C.c_int, C.c_int]),
     ("allie_attn_varlen", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
       C.c_float, C.c_void_p, C.c_int, C.c_void_p]),

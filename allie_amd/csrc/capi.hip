@@ -164,13 +164,32 @@ int check_ready(const allie_model* m) {
 
 bool is_layer_kind(int kind) { return kind >= ALLIE_W_LN1_G && kind <= ALLIE_W_PR_B; }
 
+// fp32 partial sums of the K-split GEMMs of a forward over T token rows
+// whose heads run over heads_rows rows (small M only; 0 when none splits).
+size_t part_bytes(const allie_model* m, int T, int heads_rows) {
+  if (!m->act_bf16) return 0;
+  const int d = m->d;
+  size_t mx = 0;
+  auto need = [&](int M, int N, int K) {
+    const int s = gemm_split_factor(M, N, K);
+    const size_t b = s > 1 ? (size_t)s * M * N * 4 : 0;
+    mx = b > mx ? b : mx;
+  };
+  need(T, 3 * d, d);
+  need(T, d, d);
+  need(T, 4 * d, d);
+  need(T, d, 4 * d);
+  need(heads_rows, m->NH, d);
+  return mx;
+}
+
 // Workspace of a prefill of B games / T tokens.
 struct PrefillWS {
   int32_t *lens, *cu, *ids, *pos, *seq_of, *last, *blk_off, *tiles, *status, *slot;
   int64_t* in_off;
   float* h;
   void *x, *qkv, *attn, *ff, *hx;
-  float* z;
+  float *z, *part;
   size_t total;
 };
 
@@ -202,12 +221,14 @@ PrefillWS layout_prefill(const allie_model* m, int B, int T, char* base) {
   w.ff = take((size_t)T * 4 * d * a);
   w.hx = take((size_t)B * d * a);
   w.z = (float*)take((size_t)B * m->NH * 4);
+  w.part = (float*)take(part_bytes(m, T, B));
   w.total = off;
   return w;
 }
 
+// part: workspace of the K-split partial sums (part_bytes), or null
 int gemm(const allie_model* m, const void* A, const void* W, const float* bias, const float* scale,
-         void* C, float* R, int M, int N, int K, int epi, int probe_kind, hipStream_t st) {
+         void* C, float* R, int M, int N, int K, int epi, int probe_kind, float* part, hipStream_t st) {
   GemmArgs g{};
   g.A = A;
   g.W = W;
@@ -224,6 +245,8 @@ int gemm(const allie_model* m, const void* A, const void* W, const float* bias, 
   g.epi = epi;
   g.wtype = m->cfg.mode == ALLIE_MODE_FP32 ? W_F32 : (m->cfg.mode == ALLIE_MODE_FP8W ? W_FP8 : W_BF16);
   g.out_f32 = m->cfg.mode == ALLIE_MODE_FP32;
+  g.split = (part && g.wtype != W_F32) ? gemm_split_factor(M, N, K) : 1;
+  g.part = part;
   HIP_TRY(probe_mark(probe_kind, true, st));
   hipError_t e = launch_gemm(g, st);
   if (e != hipSuccess) return fail(ALLIE_ERR_HIP, "gemm M=%d N=%d K=%d: %s", M, N, K, hipGetErrorString(e));
@@ -238,6 +261,7 @@ struct Acts {
   void* qkv;  // [T][3d]
   void* attn; // [T][d]
   void* ff;   // [T][4d]
+  float* part;  // K-split partial sums (part_bytes)
 };
 
 // The transformer blocks over T rows whose embeddings (h) and first ln_1 (x)
@@ -258,7 +282,7 @@ int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slo
   int rc;
   for (int li = 0; li < L; ++li) {
     const LayerW& l = m->layers[li];
-    if ((rc = gemm(m, w.x, l.w_qkv, l.b_qkv, l.s_qkv, w.qkv, nullptr, T, 3 * d, d, EPI_STORE, ALLIE_PROBE_QKV, st))) return rc;
+    if ((rc = gemm(m, w.x, l.w_qkv, l.b_qkv, l.s_qkv, w.qkv, nullptr, T, 3 * d, d, EPI_STORE, ALLIE_PROBE_QKV, w.part, st))) return rc;
     if (kv_pool && kv_slot) {
       KVWriteArgs kw{};
       kw.qkv = w.qkv;
@@ -274,12 +298,12 @@ int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slo
       HIP_TRY(launch_kv_write(kw, st));
     }
     if ((rc = attn(li))) return rc;
-    if ((rc = gemm(m, w.attn, l.w_o, l.b_o, l.s_o, nullptr, w.h, T, d, d, EPI_RESID, ALLIE_PROBE_PROJ, st))) return rc;
+    if ((rc = gemm(m, w.attn, l.w_o, l.b_o, l.s_o, nullptr, w.h, T, d, d, EPI_RESID, ALLIE_PROBE_PROJ, w.part, st))) return rc;
     ln.g = l.ln2_g;
     ln.b = l.ln2_b;
     HIP_TRY(launch_layernorm(ln, st));
-    if ((rc = gemm(m, w.x, l.w_fc, l.b_fc, l.s_fc, w.ff, nullptr, T, 4 * d, d, EPI_GELU, ALLIE_PROBE_FC, st))) return rc;
-    if ((rc = gemm(m, w.ff, l.w_pr, l.b_pr, l.s_pr, nullptr, w.h, T, d, 4 * d, EPI_RESID, ALLIE_PROBE_FC2, st))) return rc;
+    if ((rc = gemm(m, w.x, l.w_fc, l.b_fc, l.s_fc, w.ff, nullptr, T, 4 * d, d, EPI_GELU, ALLIE_PROBE_FC, w.part, st))) return rc;
+    if ((rc = gemm(m, w.ff, l.w_pr, l.b_pr, l.s_pr, nullptr, w.h, T, d, 4 * d, EPI_RESID, ALLIE_PROBE_FC2, w.part, st))) return rc;
     if (li + 1 < L) {
       ln.g = m->layers[li + 1].ln1_g;
       ln.b = m->layers[li + 1].ln1_b;
@@ -294,7 +318,7 @@ int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slo
 // [rows][NH] are scratch.
 int run_heads(const allie_model* m, const float* h, const int32_t* row_idx, int rows, void* hx, float* z,
               float temperature, const uint32_t* legal, int legal_words, const allie_outputs* out,
-              hipStream_t st) {
+              float* part, hipStream_t st) {
   const int d = m->d, act = m->act_bf16;
   LNArgs lf{};
   lf.h = h;
@@ -321,6 +345,8 @@ int run_heads(const allie_model* m, const float* h, const int32_t* row_idx, int 
     g.epi = EPI_STORE;
     g.wtype = act ? W_BF16 : W_F32;
     g.out_f32 = 1;
+    g.split = (part && act) ? gemm_split_factor(rows, g.N, d) : 1;
+    g.part = part;
     hipError_t e = launch_gemm(g, st);
     if (e != hipSuccess) return fail(ALLIE_ERR_HIP, "heads gemm: %s", hipGetErrorString(e));
   }
@@ -351,7 +377,7 @@ struct ExtendWS {
   int32_t *group_start, *tiles, *self_slot, *status;
   float* h;
   void *x, *qkv, *attn, *ff, *hx;
-  float* z;
+  float *z, *part;
   size_t total;
 };
 
@@ -375,6 +401,7 @@ ExtendWS layout_extend(const allie_model* m, int n, int G, char* base) {
   w.ff = take((size_t)n * 4 * d * a);
   w.hx = take((size_t)n * d * a);
   w.z = (float*)take((size_t)n * m->NH * 4);
+  w.part = (float*)take(part_bytes(m, n, n));
   w.total = off;
   return w;
 }
@@ -706,7 +733,7 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
   aa.out = w.attn;
   aa.act_bf16 = act;
 
-  const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff};
+  const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff, w.part};
   rc = run_layers(m, acts, (int)T, kv_pool ? w.slot : nullptr, kv_pool, kv_pool_blocks,
                   [&](int) -> int {
                     HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, true, st));
@@ -717,7 +744,7 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
                   st);
   if (rc) return rc;
   // heads on the last token of every game
-  return run_heads(m, w.h, w.last, n_seq, w.hx, w.z, temperature, legal, legal_words, out, st);
+  return run_heads(m, w.h, w.last, n_seq, w.hx, w.z, temperature, legal, legal_words, out, w.part, st);
 }
 
 size_t allie_extend_workspace_bytes(const allie_model* m, int n_tok, int n_groups) {
@@ -825,7 +852,7 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   xa.out = w.attn;
   xa.act_bf16 = act;
 
-  const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff};
+  const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff, w.part};
   rc = run_layers(m, acts, n_tok, w.self_slot, kv_pool, kv_pool_blocks,
                   [&](int layer) -> int {
                     xa.layer = layer;
@@ -845,7 +872,7 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
                   },
                   st);
   if (rc) return rc;
-  return run_heads(m, w.h, nullptr, n_tok, w.hx, w.z, temperature, legal, legal_words, out, st);
+  return run_heads(m, w.h, nullptr, n_tok, w.hx, w.z, temperature, legal, legal_words, out, w.part, st);
 }
 
 int allie_probe_begin(int kind, int max_launches) {
@@ -913,6 +940,45 @@ int allie_gemm(const void* A, const void* W, const float* bias, const float* sca
   HIP_TRY(launch_gemm(g, (hipStream_t)stream));
   return ALLIE_OK;
 }
+
+int allie_gemm_splitk(const void* A, const void* W, const float* bias, const float* scale, void* C,
+                      float* R, int M, int N, int K, int epi, int wtype, int out_f32, int split_k,
+                      float* part, size_t part_bytes_, void* stream) {
+  if (!A || !W || M <= 0 || N <= 0 || K <= 0 || !part) return fail(ALLIE_ERR_ARG, "bad gemm arguments");
+  if (epi < EPI_STORE || epi > EPI_RESID || (wtype != W_BF16 && wtype != W_FP8))
+    return fail(ALLIE_ERR_ARG, "bad split-K gemm mode");
+  if ((epi == EPI_RESID && !R) || (epi != EPI_RESID && !C) || (wtype == W_FP8 && !scale))
+    return fail(ALLIE_ERR_ARG, "missing gemm output/scale");
+  if (out_f32 && (wtype == W_FP8 || epi != EPI_STORE))
+    return fail(ALLIE_ERR_ARG, "fp32 output only with bf16 weights and the store epilogue");
+  const int s = split_k > 0 ? split_k : gemm_split_factor(M, N, K);
+  if (N % 128 != 0 || K % 32 != 0 || (K / 32) % s != 0)
+    return fail(ALLIE_ERR_ARG, "split-K gemm needs N %% 128 == 0, K %% 32 == 0 and K / 32 divisible by %d", s);
+  if (part_bytes_ < (size_t)s * M * N * 4)
+    return fail(ALLIE_ERR_WORKSPACE, "partials need %zu bytes", (size_t)s * M * N * 4);
+  GemmArgs g{};
+  g.A = A;
+  g.W = W;
+  g.bias = bias;
+  g.scale = scale;
+  g.C = C;
+  g.R = R;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.lda = K;
+  g.ldc = N;
+  g.ldr = N;
+  g.epi = epi;
+  g.wtype = wtype;
+  g.out_f32 = out_f32;
+  g.split = s;
+  g.part = part;
+  HIP_TRY(launch_gemm(g, (hipStream_t)stream));
+  return ALLIE_OK;
+}
+
+int allie_gemm_split_factor(int M, int N, int K) { return gemm_split_factor(M, N, K); }
 
 int allie_attn_varlen(const void* qkv, const int32_t* cu_seqlens, const int32_t* tiles,
                       int n_tiles, int n_seq, int n_tokens, int n_head, int head_dim,

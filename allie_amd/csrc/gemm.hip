@@ -137,7 +137,11 @@ ALLIE_DEV u32x4_t fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
   return o;
 }
 
-template <int EPI, int WT, bool OUT_F32>
+// output of the MFMA kernel: bf16 through LDS, fp32 rows (heads), or the
+// fp32 partial sums of one K split (reduced by splitk_reduce_kernel)
+enum { OUT_BF16 = 0, OUT_F32 = 1, OUT_PART = 2 };
+
+template <int EPI, int WT, int OUT>
 __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
   // one LDS arena: the ring of A stages, the ring of W stages; the epilogue
   // reuses it to transpose the output tile
@@ -150,12 +154,17 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (LDS-DMA base)
+  constexpr bool PART = OUT == OUT_PART;
   const int num_tm = (a.M + BM - 1) / BM, num_tn = a.N / BN;
+  // K splits: block b computes split b / tiles of tile b % tiles
+  const int n_tiles = PART ? gridDim.x / a.split : gridDim.x;
+  const int split_id = PART ? blockIdx.x / n_tiles : 0;
   int tm, tn;
-  tile_coords(blockIdx.x, gridDim.x, num_tm, num_tn, tm, tn);
+  tile_coords(PART ? blockIdx.x - split_id * n_tiles : blockIdx.x, n_tiles, num_tm, num_tn, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int K = a.K;
-  const int KT = K / BK;
+  const int KT = K / BK / (PART ? a.split : 1);  // k-tiles of this block
+  const int k_begin = split_id * KT * BK;
 
   // ---- loader geometry ----------------------------------------------------
   // bf16 rows of 64 B, 16 rows per DMA instruction: lane -> row lane / 4,
@@ -171,17 +180,17 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
   for (int i = 0; i < 4; ++i) {
     int m = m0 + wave * 64 + 16 * i + lr16;
     m = m < a.M ? m : a.M - 1;
-    a_src[i] = A + (int64_t)m * a.lda + lc16 * 8;
+    a_src[i] = A + (int64_t)m * a.lda + lc16 * 8 + k_begin;
   }
   const bf16_t* __restrict__ Wb = reinterpret_cast<const bf16_t*>(a.W);
-  const bf16_t* w_src = Wb + (int64_t)(n0 + wave * 32 + lr16) * K + lc16 * 8;
+  const bf16_t* w_src = Wb + (int64_t)(n0 + wave * 32 + lr16) * K + lc16 * 8 + k_begin;
   const int64_t w_step16 = (int64_t)16 * K;
   // fp8 rows of 32 B, 32 rows per DMA instruction: lane -> row lane / 2,
   // physical chunk lane % 2; wave w fills rows [32 w, 32 w + 32).
   const int lr8 = lane >> 1;
   const int lc8 = (lane & 1) ^ ((lr8 >> 3) & 1);
   const uint8_t* __restrict__ W8 = reinterpret_cast<const uint8_t*>(a.W);
-  const uint8_t* w8_src = W8 + (int64_t)(n0 + wave * 32 + lr8) * K + lc8 * 16;
+  const uint8_t* w8_src = W8 + (int64_t)(n0 + wave * 32 + lr8) * K + lc8 * 16 + k_begin;
 
   auto issue = [&](int kt, int s) {
     const int k0 = kt * BK;
@@ -202,12 +211,13 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
   // accumulator element (i, j, q, e) is output (m, n) with
   // m = m0 + wm 128 + j 32 + frow, n = n_base + i 32 + q 8 + half 4 + e.
   // bf16 weights: the accumulators start at the bias (fp8 weights scale the
-  // sum first, so their bias is added in the epilogue).
+  // sum first, so their bias is added in the epilogue; K splits add it in
+  // the reduction).
   f32x16_t acc[FN][FM];
 #pragma unroll
   for (int i = 0; i < FN; ++i) {
     f32x16_t init{};
-    if (!FP8 && a.bias) {
+    if (!FP8 && !PART && a.bias) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const float4 b = *reinterpret_cast<const float4*>(a.bias + n_base + i * 32 + q * 8 + half * 4);
@@ -319,8 +329,11 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
   }
 
   // ---- epilogue ------------------------------------------------------------
-  if constexpr (OUT_F32) {
-    // heads (small M): direct 16-byte stores of fp32 rows (bias already in acc)
+  if constexpr (OUT != OUT_BF16) {
+    // heads (small M) and K-split partials: direct 16-byte stores of fp32
+    // rows (the heads' bias already in acc)
+    float* Cf = PART ? a.part + (int64_t)split_id * a.M * a.N : reinterpret_cast<float*>(a.C);
+    const int64_t ldc = PART ? a.N : a.ldc;
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
 #pragma unroll
@@ -330,7 +343,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
         for (int j = 0; j < FM; ++j) {
           const int m = m0 + wm * 128 + j * 32 + frow;
           if (m >= a.M) continue;
-          *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.C) + (int64_t)m * a.ldc + n) =
+          *reinterpret_cast<float4*>(Cf + (int64_t)m * ldc + n) =
               make_float4(acc[i][j][q * 4 + 0], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
         }
       }
@@ -503,11 +516,79 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs a) {
   }
 }
 
-template <int EPI, int WT, bool OUT_F32>
+// Sum of the K splits' partials (in split order) and the epilogue, 4
+// consecutive outputs of one row per thread.
+template <int EPI, bool FP8, bool F32OUT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a) {
+  const int n4 = a.N >> 2;
+  const int64_t mn4 = (int64_t)a.M * n4;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= mn4) return;
+  const int m = (int)(idx / n4), n = (int)(idx - (int64_t)m * n4) * 4;
+  const float4* p = reinterpret_cast<const float4*>(a.part) + idx;
+  float4 v = p[0];
+  for (int s = 1; s < a.split; ++s) {
+    const float4 t = p[s * mn4];
+    v.x += t.x;
+    v.y += t.y;
+    v.z += t.z;
+    v.w += t.w;
+  }
+  if constexpr (FP8) {
+    const float4 sc = *reinterpret_cast<const float4*>(a.scale + n);
+    v.x *= sc.x;
+    v.y *= sc.y;
+    v.z *= sc.z;
+    v.w *= sc.w;
+  }
+  if (a.bias) {
+    const float4 b = *reinterpret_cast<const float4*>(a.bias + n);
+    v.x += b.x;
+    v.y += b.y;
+    v.z += b.z;
+    v.w += b.w;
+  }
+  if constexpr (F32OUT) {
+    *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.C) + (int64_t)m * a.ldc + n) = v;
+  } else if constexpr (EPI == EPI_RESID) {
+    round_bf16x2(v.x, v.y);
+    round_bf16x2(v.z, v.w);
+    float4* r = reinterpret_cast<float4*>(a.R + (int64_t)m * a.ldr + n);
+    float4 h = *r;
+    h.x += v.x;
+    h.y += v.y;
+    h.z += v.z;
+    h.w += v.w;
+    *r = h;
+  } else {
+    if constexpr (EPI == EPI_GELU) {
+      round_bf16x2(v.x, v.y);
+      round_bf16x2(v.z, v.w);
+      v.x = gelu_tanh_fast(v.x);
+      v.y = gelu_tanh_fast(v.y);
+      v.z = gelu_tanh_fast(v.z);
+      v.w = gelu_tanh_fast(v.w);
+    }
+    uint2 pk;
+    pk.x = pack_bf16x2(v.x, v.y);
+    pk.y = pack_bf16x2(v.z, v.w);
+    *reinterpret_cast<uint2*>(reinterpret_cast<bf16_t*>(a.C) + (int64_t)m * a.ldc + n) = pk;
+  }
+}
+
+template <int EPI, int WT, bool F32OUT>
 hipError_t launch_mfma(const GemmArgs& a, hipStream_t st) {
   const int num_tm = (a.M + BM - 1) / BM, num_tn = a.N / BN;
-  hipLaunchKernelGGL((gemm_mfma_kernel<EPI, WT, OUT_F32>), dim3(num_tm * num_tn), dim3(NTHREADS),
-                     0, st, a);
+  const int tiles = num_tm * num_tn;
+  if (a.split > 1) {
+    hipLaunchKernelGGL((gemm_mfma_kernel<EPI, WT, OUT_PART>), dim3(tiles * a.split), dim3(NTHREADS), 0, st, a);
+    const int64_t n4 = (int64_t)a.M * (a.N / 4);
+    hipLaunchKernelGGL((splitk_reduce_kernel<EPI, WT == W_FP8, F32OUT>), dim3((unsigned)((n4 + 255) / 256)),
+                       dim3(256), 0, st, a);
+  } else {
+    hipLaunchKernelGGL((gemm_mfma_kernel<EPI, WT, F32OUT ? OUT_F32 : OUT_BF16>), dim3(tiles), dim3(NTHREADS), 0,
+                       st, a);
+  }
   return hipGetLastError();
 }
 
@@ -517,6 +598,17 @@ namespace allie {
 
 bool gemm_mfma_supported(const GemmArgs& a) {
   return a.N % BN == 0 && a.K % BK == 0 && a.lda % 8 == 0 && a.M > 0;
+}
+
+int gemm_split_factor(int M, int N, int K) {
+  if (M <= 0 || N % BN != 0 || K % BK != 0) return 1;
+  const int64_t tiles = (int64_t)((M + BM - 1) / BM) * (N / BN);
+  const int KT = K / BK;
+  int s = 1;
+  // double while the grid stays within one block per CU of a 256-CU device
+  // and every split keeps at least 8 k-tiles
+  while (s < 8 && tiles * s * 2 <= 256 && KT % (s * 2) == 0 && KT / (s * 2) >= 8) s *= 2;
+  return s;
 }
 
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t st) {
@@ -532,6 +624,7 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t st) {
     return hipGetLastError();
   }
   if (!gemm_mfma_supported(a)) return hipErrorInvalidValue;
+  if (a.split > 1 && (a.part == nullptr || (a.K / BK) % a.split != 0)) return hipErrorInvalidValue;
   if (a.wtype == W_BF16) {
     switch (a.epi) {
       case EPI_STORE:

@@ -81,9 +81,14 @@ struct GemmArgs {
   int epi;
   int wtype;
   int out_f32;         // store C as fp32 (else bf16)
+  int split;           // K splits (MFMA kernels; <= 1: none)
+  float* part;         // [split][M][N] fp32 partial sums when split > 1
 };
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t st);
 bool gemm_mfma_supported(const GemmArgs& a);
+// K splits the forward uses for an M x N x K MFMA GEMM: enough blocks for
+// every CU when the output tiles alone leave most idle (small M)
+int gemm_split_factor(int M, int N, int K);
 
 // ------------------------------------------------------------- attention
 // Varlen causal self-attention over packed sequences (no KV cache):

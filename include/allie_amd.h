@@ -209,6 +209,16 @@ int allie_probe_end(float* total_ms_host, int* n_launches_host);
  * (0 store, 1 gelu, 2 residual add into R fp32); wtype 0 bf16, 1 fp32, 2 fp8. */
 int allie_gemm(const void* A, const void* W, const float* bias, const float* scale, void* C,
                float* R, int M, int N, int K, int epi, int wtype, int out_f32, void* stream);
+/* The same GEMM with K split into split_k parts (0: the split the forward
+ * picks for this shape, allie_gemm_split_factor) whose fp32 partial sums go
+ * to part (split * M * N floats), then one reduction pass applies the
+ * epilogue.  bf16 or fp8 weights.  The forward splits small-M GEMMs this way
+ * (decode steps, tree levels: the output tiles alone would leave most CUs
+ * idle); the split count is fixed per shape, so results are deterministic. */
+int allie_gemm_splitk(const void* A, const void* W, const float* bias, const float* scale, void* C,
+                      float* R, int M, int N, int K, int epi, int wtype, int out_f32, int split_k,
+                      float* part, size_t part_bytes, void* stream);
+int allie_gemm_split_factor(int M, int N, int K);
 int allie_attn_varlen(const void* qkv, const int32_t* cu_seqlens, const int32_t* tiles,
                       int n_tiles, int n_seq, int n_tokens, int n_head, int head_dim,
                       float scale, void* out, int act_bf16, void* stream);

@@ -163,6 +163,61 @@ def test_gemm_bf16_epilogues(M, N, K, cuda):
     assert ((R - (R0 + acc)).abs() <= acc.abs() * 2 ** -8 + 1e-5).all()
 
 
+def _gemm_split(A, Wt, bias, epi, wtype, split, out_f32=False, R=None, scale=None):
+    M, K = A.shape
+    N = Wt.shape[0]
+    s = split if split > 0 else L.allie_gemm_split_factor(M, N, K)
+    part = torch.empty(max(s, 1) * M * N, dtype=torch.float32, device=A.device)
+    C_ = None
+    if epi != capi.EPI_RESID:
+        C_ = torch.empty(M, N, dtype=torch.float32 if out_f32 else torch.bfloat16, device=A.device)
+    rc = L.allie_gemm_splitk(capi.ptr(A), capi.ptr(Wt), capi.ptr(bias), capi.ptr(scale), capi.ptr(C_),
+                             capi.ptr(R), M, N, K, epi, wtype, int(out_f32), split, capi.ptr(part),
+                             part.numel() * 4, capi.stream_ptr())
+    capi.check(rc, "gemm_splitk")
+    torch.cuda.synchronize()
+    return C_
+
+
+# (M, N, K, split): 0 = the forward's own choice (8 for the decode-step MLP
+# c_proj), ragged last m-tile, the heads' fp32 output
+SPLIT_CASES = [(1024, 1024, 4096, 0), (300, 3072, 1024, 4), (1000, 1024, 1024, 2), (256, 2048, 1024, 4),
+               (77, 512, 2048, 16)]
+
+
+@pytest.mark.parametrize("M,N,K,split", SPLIT_CASES)
+def test_gemm_split_k(M, N, K, split, cuda):
+    """K-split partial sums plus the reduction pass, against the same torch
+    fp32 reference and bars as the unsplit GEMM; repeated calls are bit-identical."""
+    g = torch.Generator(device="cpu").manual_seed(M + N + K + split)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16).to(cuda)
+    Wt = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16).to(cuda)
+    b = rb(torch.randn(N, generator=g) * 0.1).to(cuda)
+    acc = A.float() @ Wt.float().T + b
+    C_ = _gemm_split(A, Wt, b, capi.EPI_STORE, capi.WT_BF16, split).float()
+    assert ((C_ - acc).abs() <= acc.abs() * 2 ** -8 + 1e-5).all()
+    C2 = _gemm_split(A, Wt, b, capi.EPI_STORE, capi.WT_BF16, split).float()
+    assert torch.equal(C_, C2)
+    C32 = _gemm_split(A, Wt, b, capi.EPI_STORE, capi.WT_BF16, split, out_f32=True)
+    torch.testing.assert_close(C32, acc, rtol=1e-5, atol=1e-4)
+    Cg = _gemm_split(A, Wt, b, capi.EPI_GELU, capi.WT_BF16, split).float()
+    t = rb(acc)
+    ref = (0.5 * t) * (1 + torch.tanh(math.sqrt(2 / math.pi) * (t + 0.044715 * t ** 3)))
+    assert ((Cg - ref).abs() <= ref.abs() * 2 ** -6 + 2e-3).all()
+    R0 = torch.randn(M, N, generator=g).to(cuda)
+    R = R0.clone()
+    _gemm_split(A, Wt, b, capi.EPI_RESID, capi.WT_BF16, split, R=R)
+    assert ((R - (R0 + acc)).abs() <= acc.abs() * 2 ** -8 + 1e-5).all()
+    # fp8 weights
+    w = torch.randn(N, K, generator=g) * 0.05
+    s = (w.abs().amax(1) / 448.0).float()
+    q = (w / s[:, None]).to(torch.float8_e4m3fn)
+    accq = A.float() @ (q.float() * s[:, None]).to(cuda).T + b
+    Cq = _gemm_split(A, q.view(torch.uint8).to(cuda), b, capi.EPI_STORE, capi.WT_FP8, split,
+                     scale=s.to(cuda)).float()
+    assert ((Cq - accq).abs() <= accq.abs() * 2 ** -8 + 1e-4).all()
+
+
 @pytest.mark.parametrize("M,N", [(1000, 128), (4100, 4096)])
 def test_gemm_epilogue_rounds_to_nearest_even(M, N, cuda):
     """The bf16 epilogues round fp32 sums to nearest even, bit for bit: A's
