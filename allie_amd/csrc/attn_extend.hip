@@ -18,7 +18,8 @@
 //
 // attn_extend_wave_kernel  -- one wave per (token, head); lane l owns key
 //   l / 4 of a 16-key block and head dims 16 (l % 4) .. +15.  Streams the keys
-//   once per query: the decode kernel (groups of one token).
+//   once per query, the next block's keys and values loading while one is
+//   reduced: the decode kernel (groups of one token).
 // attn_extend_tree_kernel  -- a workgroup per (64-query tile of a group,
 //   head): the group's prefix keys are staged through LDS once per tile and
 //   multiplied on the MFMA units (S^T = K Q^T, O^T = V^T P^T, as in the
@@ -136,6 +137,39 @@ ALLIE_DEV void load16<float>(const float* p, float (&v)[16]) {
   }
 }
 
+// 16 elements of a key or value row as stored (bf16: 32 B, fp32: 64 B)
+template <typename T>
+struct Row16 {
+  uint4 v[sizeof(T) * 16 / 16];
+};
+template <typename T>
+ALLIE_DEV void fetch16(const T* p, Row16<T>& r) {
+#pragma unroll
+  for (int j = 0; j < (int)(sizeof(T)); ++j) r.v[j] = reinterpret_cast<const uint4*>(p)[j];
+}
+template <typename T>
+ALLIE_DEV void widen16(const Row16<T>& r, float (&v)[16]) {
+  if constexpr (sizeof(T) == 2) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t w[4] = {r.v[j].x, r.v[j].y, r.v[j].z, r.v[j].w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        v[8 * j + 2 * t] = bf2f(w[t] & 0xffffu);
+        v[8 * j + 2 * t + 1] = bf2f(w[t] >> 16);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[4 * j] = __uint_as_float(r.v[j].x);
+      v[4 * j + 1] = __uint_as_float(r.v[j].y);
+      v[4 * j + 2] = __uint_as_float(r.v[j].z);
+      v[4 * j + 3] = __uint_as_float(r.v[j].w);
+    }
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void attn_extend_wave_kernel(ExtendAttnArgs a) {
   const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -145,36 +179,84 @@ __global__ __launch_bounds__(256) void attn_extend_wave_kernel(ExtendAttnArgs a)
   const int lane = threadIdx.x & 63;
   const int kj = lane >> 2, dq = (lane & 3) * 16;
   // group of token i: group_start[g] <= i < group_start[g + 1]
-  int lo = 0, hi = a.n_groups;
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (a.group_start[mid] <= i) lo = mid; else hi = mid;
+  int lo = i, hi = a.n_groups;
+  if (!a.one_token_groups) {
+    lo = 0;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (a.group_start[mid] <= i) lo = mid; else hi = mid;
+    }
   }
   const int g = lo;
   const T* __restrict__ qkv = reinterpret_cast<const T*>(a.qkv);
   const T* __restrict__ pool = reinterpret_cast<const T*>(a.pool);
   const float sl2 = a.scale * 1.4426950408889634f;  // scale * log2(e)
+  // q: bf16 pairs as stored (dot products by v_dot2_f32_bf16, the scale
+  // applied to the sum), or fp32 pre-scaled
+  Row16<T> qr;
+  fetch16<T>(qkv + (int64_t)i * 3 * d + head * HD + dq, qr);
   float q[16];
-  load16<T>(qkv + (int64_t)i * 3 * d + head * HD + dq, q);
+  if constexpr (sizeof(T) == 4) {
+    widen16<T>(qr, q);
 #pragma unroll
-  for (int j = 0; j < 16; ++j) q[j] *= sl2;
+    for (int j = 0; j < 16; ++j) q[j] *= sl2;
+  }
+
+  // keys in chunks of 16 (lane's key kj of the chunk): first the visible
+  // prefix, one pool block per chunk -- positions below both the group's
+  // prefix length and the token's own position -- then the token's extras
+  const int P = min(a.prefix_len[g], a.pos[i]);
+  int nbp = (P + KV_BLOCK - 1) / KV_BLOCK;
+  nbp = nbp < a.max_blocks ? nbp : a.max_blocks;
+  int E = a.n_extra[i];
+  E = E < 0 ? 0 : (E > a.max_extra ? a.max_extra : E);
+  const int nch = nbp + (E + KV_BLOCK - 1) / KV_BLOCK;
+  const int32_t* btab = a.prefix_blocks + (int64_t)g * a.max_blocks;
+  const int my_blk = lane < nbp ? btab[lane] : -1;  // the first 64 blocks of the row
+  auto locate = [&](int c, int64_t& off, bool& ok) {
+    int blk, kpos;
+    if (c < nbp) {
+      blk = c < 64 ? __builtin_amdgcn_readlane(my_blk, c) : btab[c];
+      kpos = kj;
+      ok = c * KV_BLOCK + kj < P;
+    } else {
+      const int e = (c - nbp) * KV_BLOCK + kj;
+      const int sl = e < E ? a.extra_slot[(int64_t)i * a.max_extra + e] : -1;
+      blk = sl >> 4;
+      kpos = sl & 15;
+      ok = sl >= 0;
+    }
+    ok = ok && blk >= 0 && blk < a.pool_blocks;
+    off = pool_off(ok ? blk : 0, a.n_layer, a.layer, 0, H, head, ok ? kpos : 0) + dq;
+  };
 
   float m_run = -INFINITY, l_run = 0.f, acc[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) acc[j] = 0.f;
-
-  // one 16-key block: lane's key is (blk, off) if ok
-  auto step = [&](int64_t blk, int off, bool ok) {
-    float kv[16];
-    float s = -INFINITY;
-    if (ok) {
-      load16<T>(pool + pool_off(blk, a.n_layer, a.layer, 0, H, head, off) + dq, kv);
-      s = 0.f;
+  const int64_t voff = (int64_t)H * KV_BLOCK * HD;  // k -> v of the same (block, layer, head)
+  // one chunk's keys and values (kr, vr) into the running softmax
+  auto reduce_chunk = [&](const Row16<T>& kr, const Row16<T>& vr, bool ok) {
+    float s = 0.f;
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const uint32_t qw[4] = {qr.v[j].x, qr.v[j].y, qr.v[j].z, qr.v[j].w};
+        const uint32_t kw[4] = {kr.v[j].x, kr.v[j].y, kr.v[j].z, kr.v[j].w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qw[t]), __builtin_bit_cast(bf16x2_t, kw[t]),
+                                              s, false);
+      }
+      s *= sl2;
+    } else {
+      float kv[16];
+      widen16<T>(kr, kv);
 #pragma unroll
       for (int j = 0; j < 16; ++j) s = fmaf(q[j], kv[j], s);
     }
-    s += __shfl_xor(s, 1, 64);  // the 4 lanes of a key share ok, so -inf stays -inf
+    s += __shfl_xor(s, 1, 64);  // the 4 lanes of a key share ok
     s += __shfl_xor(s, 2, 64);
+    s = ok ? s : -INFINITY;
     float mb = s;
 #pragma unroll
     for (int o = 4; o < 64; o <<= 1) mb = fmaxf(mb, __shfl_xor(mb, o, 64));
@@ -183,28 +265,28 @@ __global__ __launch_bounds__(256) void attn_extend_wave_kernel(ExtendAttnArgs a)
     const float alpha = exp2f(m_run - m_new);
     const float p = ok ? exp2f(s - m_new) : 0.f;
     l_run = l_run * alpha + ((lane & 3) == 0 ? p : 0.f);
-    if (ok) load16<T>(pool + pool_off(blk, a.n_layer, a.layer, 1, H, head, off) + dq, kv);
+    float vv[16];
+    widen16<T>(vr, vv);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) acc[j] = acc[j] * alpha + (ok ? p * kv[j] : 0.f);
+    for (int j = 0; j < 16; ++j) acc[j] = acc[j] * alpha + p * vv[j];
     m_run = m_new;
   };
-
-  // visible prefix: positions below both the group's prefix length and the
-  // token's own position (a new game's prefix tokens see only earlier ones)
-  const int P = min(a.prefix_len[g], a.pos[i]);
-  const int nb = (P + KV_BLOCK - 1) / KV_BLOCK;
-  for (int b = 0; b < nb && b < a.max_blocks; ++b) {
-    const int blk = a.prefix_blocks[(int64_t)g * a.max_blocks + b];
-    const bool ok = blk >= 0 && blk < a.pool_blocks && b * KV_BLOCK + kj < P;
-    step(ok ? blk : 0, kj, ok);
-  }
-  int E = a.n_extra[i];
-  E = E < 0 ? 0 : (E > a.max_extra ? a.max_extra : E);
-  for (int e0 = 0; e0 < E; e0 += 16) {
-    const int e = e0 + kj;
-    const int sl = e < E ? a.extra_slot[(int64_t)i * a.max_extra + e] : -1;
-    const bool ok = sl >= 0 && (sl >> 4) < a.pool_blocks;
-    step(ok ? (sl >> 4) : 0, sl & 15, ok);
+  auto fetch_chunk = [&](int c, Row16<T>& kr, Row16<T>& vr, bool& ok) {
+    int64_t off;
+    locate(c, off, ok);
+    fetch16<T>(pool + off, kr);
+    fetch16<T>(pool + off + voff, vr);
+  };
+  // two register buffers: chunk c + 1 loads while chunk c is reduced
+  Row16<T> kA, vA, kB, vB;
+  bool okA = false, okB = false;
+  if (nch > 0) fetch_chunk(0, kA, vA, okA);
+  for (int c = 0; c < nch; c += 2) {
+    if (c + 1 < nch) fetch_chunk(c + 1, kB, vB, okB);
+    reduce_chunk(kA, vA, okA);
+    if (c + 1 >= nch) break;
+    if (c + 2 < nch) fetch_chunk(c + 2, kA, vA, okA);
+    reduce_chunk(kB, vB, okB);
   }
   // combine the 16 key lanes of each head-dim group
 #pragma unroll

@@ -834,6 +834,7 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   xa.qkv = w.qkv;
   xa.pos = pos;
   xa.n = n_tok;
+  xa.one_token_groups = n1 == n_groups;
   xa.n_head = m->H;
   xa.group_start = w.group_start;
   xa.n_groups = n_groups;
@@ -861,6 +862,7 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
                       if (n1 > 0) {
                         ExtendAttnArgs wa = xa;
                         wa.n = n1;
+                        wa.one_token_groups = 1;
                         HIP_TRY(launch_attn_extend_wave(wa, st));
                       }
                       HIP_TRY(launch_attn_extend_tree(xa, st));

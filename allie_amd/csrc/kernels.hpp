@@ -133,6 +133,7 @@ struct ExtendAttnArgs {
   const void* qkv;             // [n][3d] new tokens (q | k | v)
   const int32_t* pos;          // [n] token positions: prefix keys at or past pos[i] are not visible
   int n, n_head;
+  int one_token_groups;        // wave kernel: token i is group i (all groups of one token)
   const int32_t* group_start;  // [G + 1]
   int n_groups;
   const int32_t* prefix_len;   // [G]
