@@ -264,13 +264,37 @@ struct Acts {
   float* part;  // K-split partial sums (part_bytes)
 };
 
+// Whether the M x N x K store GEMM of this model runs on the persistent
+// kernel (see gemm()): then the projection feeding the residual stream is
+// stored as bf16 and added in the LayerNorm that follows.
+bool store_is_persistent(const allie_model* m, int M, int N, int K, const float* part) {
+  GemmArgs g{};
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.lda = K;
+  g.ldc = N;
+  g.epi = EPI_STORE;
+  g.wtype = m->cfg.mode == ALLIE_MODE_FP32 ? W_F32 : (m->cfg.mode == ALLIE_MODE_FP8W ? W_FP8 : W_BF16);
+  g.out_f32 = m->cfg.mode == ALLIE_MODE_FP32;
+  g.split = (part && g.wtype != W_F32) ? gemm_split_factor(M, N, K) : 1;
+  return gemm_uses_persistent(g);
+}
+
 // The transformer blocks over T rows whose embeddings (h) and first ln_1 (x)
 // are in place.  kv_slot/kv_pool: every layer's keys and values of row t are
 // written to pool slot kv_slot[t] (before attention runs).  attn(layer) runs
 // the attention of one layer from acts.qkv into acts.attn.
+//
+// The attention and MLP output projections end in the residual add
+// h += bf16(y + b) (src/modeling/model.py:50-55 -> [lib] GPT2Block).  Small-M
+// GEMMs add into h in their epilogue; GEMMs on the persistent kernel store y
+// (bf16, into x) and the next LayerNorm adds it (h += y; x = LN(h)).  After
+// the last block, *final_add is the y still to be added to h (the heads'
+// ln_f adds it on the rows it reads), or null.
 template <typename AttnFn>
 int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slot, void* kv_pool,
-               int kv_pool_blocks, AttnFn&& attn, hipStream_t st) {
+               int kv_pool_blocks, AttnFn&& attn, hipStream_t st, const void** final_add) {
   const int d = m->d, L = m->L, act = m->act_bf16;
   LNArgs ln{};
   ln.h = w.h;
@@ -279,6 +303,9 @@ int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slo
   ln.eps = m->cfg.eps;
   ln.y = w.x;
   ln.act_bf16 = act;
+  const bool fuse_proj = store_is_persistent(m, T, d, d, w.part);
+  const bool fuse_fc2 = store_is_persistent(m, T, d, 4 * d, w.part);
+  *final_add = nullptr;
   int rc;
   for (int li = 0; li < L; ++li) {
     const LayerW& l = m->layers[li];
@@ -298,30 +325,46 @@ int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slo
       HIP_TRY(launch_kv_write(kw, st));
     }
     if ((rc = attn(li))) return rc;
-    if ((rc = gemm(m, w.attn, l.w_o, l.b_o, l.s_o, nullptr, w.h, T, d, d, EPI_RESID, ALLIE_PROBE_PROJ, w.part, st))) return rc;
+    if (fuse_proj) {
+      if ((rc = gemm(m, w.attn, l.w_o, l.b_o, l.s_o, w.x, nullptr, T, d, d, EPI_STORE, ALLIE_PROBE_PROJ, w.part, st))) return rc;
+    } else {
+      if ((rc = gemm(m, w.attn, l.w_o, l.b_o, l.s_o, nullptr, w.h, T, d, d, EPI_RESID, ALLIE_PROBE_PROJ, w.part, st))) return rc;
+    }
     ln.g = l.ln2_g;
     ln.b = l.ln2_b;
+    ln.add = fuse_proj ? w.x : nullptr;
+    ln.h_out = fuse_proj ? w.h : nullptr;
     HIP_TRY(launch_layernorm(ln, st));
     if ((rc = gemm(m, w.x, l.w_fc, l.b_fc, l.s_fc, w.ff, nullptr, T, 4 * d, d, EPI_GELU, ALLIE_PROBE_FC, w.part, st))) return rc;
-    if ((rc = gemm(m, w.ff, l.w_pr, l.b_pr, l.s_pr, nullptr, w.h, T, d, 4 * d, EPI_RESID, ALLIE_PROBE_FC2, w.part, st))) return rc;
+    if (fuse_fc2) {
+      if ((rc = gemm(m, w.ff, l.w_pr, l.b_pr, l.s_pr, w.x, nullptr, T, d, 4 * d, EPI_STORE, ALLIE_PROBE_FC2, w.part, st))) return rc;
+    } else {
+      if ((rc = gemm(m, w.ff, l.w_pr, l.b_pr, l.s_pr, nullptr, w.h, T, d, 4 * d, EPI_RESID, ALLIE_PROBE_FC2, w.part, st))) return rc;
+    }
     if (li + 1 < L) {
       ln.g = m->layers[li + 1].ln1_g;
       ln.b = m->layers[li + 1].ln1_b;
+      ln.add = fuse_fc2 ? w.x : nullptr;
+      ln.h_out = fuse_fc2 ? w.h : nullptr;
       HIP_TRY(launch_layernorm(ln, st));
+    } else if (fuse_fc2) {
+      *final_add = w.x;
     }
   }
   return ALLIE_OK;
 }
 
 // ln_f, the heads GEMM and the heads kernel over `rows` rows of h (row r is
-// h[row_idx[r]], or h[r] when row_idx is null); hx [rows][d] and z
-// [rows][NH] are scratch.
-int run_heads(const allie_model* m, const float* h, const int32_t* row_idx, int rows, void* hx, float* z,
-              float temperature, const uint32_t* legal, int legal_words, const allie_outputs* out,
+// h[row_idx[r]], or h[r] when row_idx is null; plus h_add's row when the last
+// block's residual add is still pending); hx [rows][d] and z [rows][NH] are
+// scratch.
+int run_heads(const allie_model* m, const float* h, const void* h_add, const int32_t* row_idx, int rows, void* hx,
+              float* z, float temperature, const uint32_t* legal, int legal_words, const allie_outputs* out,
               float* part, hipStream_t st) {
   const int d = m->d, act = m->act_bf16;
   LNArgs lf{};
   lf.h = h;
+  lf.add = h_add;
   lf.row_idx = row_idx;
   lf.rows = lf.rows_out = rows;
   lf.d = d;
@@ -734,6 +777,7 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
   aa.act_bf16 = act;
 
   const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff, w.part};
+  const void* final_add = nullptr;
   rc = run_layers(m, acts, (int)T, kv_pool ? w.slot : nullptr, kv_pool, kv_pool_blocks,
                   [&](int) -> int {
                     HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, true, st));
@@ -741,10 +785,10 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
                     HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, false, st));
                     return ALLIE_OK;
                   },
-                  st);
+                  st, &final_add);
   if (rc) return rc;
   // heads on the last token of every game
-  return run_heads(m, w.h, w.last, n_seq, w.hx, w.z, temperature, legal, legal_words, out, w.part, st);
+  return run_heads(m, w.h, final_add, w.last, n_seq, w.hx, w.z, temperature, legal, legal_words, out, w.part, st);
 }
 
 size_t allie_extend_workspace_bytes(const allie_model* m, int n_tok, int n_groups) {
@@ -854,6 +898,7 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   xa.act_bf16 = act;
 
   const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff, w.part};
+  const void* final_add = nullptr;
   rc = run_layers(m, acts, n_tok, w.self_slot, kv_pool, kv_pool_blocks,
                   [&](int layer) -> int {
                     xa.layer = layer;
@@ -872,9 +917,9 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
                     HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, false, st));
                     return ALLIE_OK;
                   },
-                  st);
+                  st, &final_add);
   if (rc) return rc;
-  return run_heads(m, w.h, nullptr, n_tok, w.hx, w.z, temperature, legal, legal_words, out, w.part, st);
+  return run_heads(m, w.h, final_add, nullptr, n_tok, w.hx, w.z, temperature, legal, legal_words, out, w.part, st);
 }
 
 int allie_probe_begin(int kind, int max_launches) {

@@ -52,6 +52,8 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <type_traits>
+
 namespace {
 
 using namespace allie;
@@ -102,10 +104,11 @@ ALLIE_DEV void wait_vm_tiles(int n_tiles) {
   switch (n_tiles) {
     case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
     case 1: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(VMT) : "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * VMT) : "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * VMT) : "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * VMT) : "memory"); break;
   }
 }
-static_assert(STAGES - 1 <= 2, "wait_vm_tiles covers up to two newer tiles in flight");
+static_assert(STAGES - 1 <= 3, "wait_vm_tiles covers up to three newer tiles in flight");
 
 // Workgroup barrier without a memory fence: LDS reads issued before it have
 // completed (lgkmcnt(0)); the compiler may not move memory accesses across it.
@@ -443,6 +446,349 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Large GEMMs (the prefill's QKV, attention c_proj, c_fc and MLP c_proj over
+// tens of thousands of tokens, bf16 weights, bf16 output): a persistent
+// kernel, one block of 4 waves per CU, block tile 256 (m) x 256 (n).  Each
+// wave owns 128 x 128 = 4 x 4 MFMA 32x32x16 blocks; its 256 fp32
+// accumulators live in the accumulation registers (one wave per SIMD has 512
+// registers).  Against the 256 x 128 kernel above, a tile moves 128 instead
+// of 85 FLOP per byte through L2, and a wave issues 8 fragment reads per 16
+// MFMAs instead of 6 per 8.
+//
+// k-tiles of 64: every row of a stage is one whole 128-byte line of A or W,
+// so each request fetches a full line.  Two stages (128 KiB): tile kt + 2
+// loads while tiles kt and kt + 1 are multiplied.  The loads are buffer
+// loads straight to LDS over the tile's own rows: rows past M read as 0, the
+// row is in the per-lane offset and the k offset in the scalar one.
+//
+// Persistent tile loop: as soon as a tile's last k-tile is multiplied, the
+// next tile's bias and first two k-tiles are requested, and only then is the
+// finished tile written out, so the loads of the next tile are in flight
+// during the epilogue.  The epilogue goes through a separate wave-private
+// LDS region in chunks of 32 rows x 64 columns (rows of 128 bytes to global
+// memory) with buffer stores, which are always issued (rows past M fall
+// outside the buffer and are dropped), so every wave has exactly STORES
+// stores in flight when the next tile's waits count its loads.
+//
+// k order inside a k-tile: in MFMA step s (0..3) the lanes of half h multiply
+// logical chunk 2 s + h (k = 16 s + 8 h .. +7), identically for both
+// operands.  LDS rows of 128 B (8 chunks): chunk c of row r sits at
+// c ^ ((r >> 1) & 7), so 16 consecutive rows reading one chunk hit 16
+// distinct 16-byte bank groups (rows r and r + 1 fill opposite halves of the
+// 64 banks).  Epilogues: EPI_STORE C = bf16(acc + b), EPI_GELU
+// C = bf16(gelu(bf16(acc + b))).
+namespace big {
+constexpr int BM = 256, BN = 256, BK = 64, STAGES = 2;
+constexpr int FM = 4, FN = 4;       // 32x32 MFMA blocks per wave along m and n
+constexpr int A_STAGE = BM * BK;    // bf16 elements per stage (32 KiB each)
+constexpr int W_STAGE = BN * BK;
+constexpr int RING = STAGES * (A_STAGE + W_STAGE);  // 128 KiB
+constexpr int DMA = 8;              // DMA instructions per wave per k-tile and operand
+constexpr int EP = 72;              // epilogue chunk row pitch (bf16)
+constexpr int CHUNK = 32 * EP;      // one wave's epilogue region (bf16 elements)
+constexpr int BIAS = RING + 4 * CHUNK;  // 256 fp32 bias values of the tile
+constexpr int SMEM = BIAS + 4 * BN;     // bf16 elements: + a spare bias slot (149 KiB)
+constexpr int STORES = 32;          // epilogue stores per wave per tile
+
+// element offset of logical 16-byte chunk c of row r in a stage
+ALLIE_DEV int swz(int r, int c) { return r * BK + ((c ^ ((r >> 1) & 7)) << 3); }
+
+// s_waitcnt vmcnt(N): at most N of this wave's vector-memory operations in flight
+template <int N>
+ALLIE_DEV void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+}  // namespace big
+
+typedef __attribute__((address_space(3))) void lds_void_t2;
+
+// The value unchanged, but opaque to the optimizer: keeps address arithmetic
+// inside the tile loop instead of dozens of hoisted registers.
+ALLIE_DEV int opaque_s(int v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+ALLIE_DEV int opaque_v(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+// 16-byte LDS read the compiler's wait insertion does not track: the caller
+// waits (lgkmcnt) before using the result.  Used where the compiler would
+// otherwise wait for every outstanding LDS DMA load.
+ALLIE_DEV float4 lds_read_f4(const void* p) {
+  float4 r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p) : "memory");
+  return r;
+}
+ALLIE_DEV uint32_t lds_off(const void* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+ALLIE_DEV void lds_write_b64(void* p, uint2 v) {
+  asm volatile("ds_write_b64 %0, %1" ::"v"(lds_off(p)), "v"(v) : "memory");
+}
+ALLIE_DEV u32x4_t lds_read_b128(const void* p) {
+  u32x4_t r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(lds_off(p)) : "memory");
+  return r;
+}
+// An accumulator read where it is used (not all 256 copied out at once
+// after the k-loop)
+ALLIE_DEV float acc_read(float v) {
+  float r;
+  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(r) : "a"(v));
+  return r;
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  // the 256 x 256 geometry (shadows the 256 x 128 kernel's constants)
+  constexpr int BM = big::BM, BN = big::BN, BK = big::BK;
+  constexpr int FM = big::FM, FN = big::FN, A_STAGE = big::A_STAGE, W_STAGE = big::W_STAGE;
+  constexpr int DMA = big::DMA, EP = big::EP;
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[big::SMEM];
+  auto sA = [&](int s) { return smem + s * A_STAGE; };
+  auto sW = [&](int s) { return smem + big::STAGES * A_STAGE + s * W_STAGE; };
+  const float* bias_lds = reinterpret_cast<const float*>(smem + big::BIAS);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int num_tm = (a.M + BM - 1) / BM, num_tn = a.N / BN;
+  const int tiles = num_tm * num_tn;
+  const int K = a.K, KT = K / BK;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int frow = lane & 31, half = lane >> 5;
+
+  // loader: one DMA instruction fills 8 rows of 128 B (lane -> row lane / 8,
+  // physical chunk lane % 8); wave w fills rows [64 w, 64 w + 64) of both
+  // the A and the W stage.  Row 64 w + 8 i + lane / 8 holds logical chunk
+  // (lane % 8) ^ ((4 i + lane / 16) & 7) in that physical slot.
+  const int lc_even = (lane & 7) ^ (lane >> 4);
+  // A loads: instruction i reads row 64 w + 8 i + lane / 8 (per-lane offset,
+  // so that rows past M fall outside the buffer)
+  const uint32_t a_lane = (uint32_t)((wave * 64 + (lane >> 3)) * a.lda * 2);
+  const uint32_t a_ev = a_lane + lc_even * 16, a_od = a_lane + (lc_even ^ 4) * 16;
+
+  // W loads: the row group of instruction i goes into the scalar offset
+  // (every W row of a tile is valid); two per-lane offsets (even and odd i)
+  const uint32_t w_lane = (uint32_t)((lane >> 3) * K * 2);
+  const uint32_t w_ev = w_lane + lc_even * 16, w_od = w_lane + (lc_even ^ 4) * 16;
+
+  // per-tile buffers: A over the tile's rows (rows past M read 0), W over
+  // its 256 rows, C over its rows (stores past M dropped), the bias slice
+  // (without a bias the slice is read from A, always valid, and ignored)
+  struct Tile {
+    int m0, n0, rows;
+  };
+  auto make_tile = [&](int t) {
+    Tile T;
+    int tm, tn;
+    tile_coords(t, tiles, num_tm, num_tn, tm, tn);
+    T.m0 = tm * BM;
+    T.n0 = tn * BN;
+    T.rows = a.M - T.m0 < BM ? a.M - T.m0 : BM;
+    return T;
+  };
+  auto rsrc_A = [&](const Tile& T) {
+    return __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16_t*>(reinterpret_cast<const bf16_t*>(a.A) + (int64_t)T.m0 * a.lda), (short)0,
+        T.rows * a.lda * 2, 0x00020000);
+  };
+  auto rsrc_W = [&](const Tile& T) {
+    return __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16_t*>(reinterpret_cast<const bf16_t*>(a.W) + (int64_t)T.n0 * K), (short)0, BN * K * 2,
+        0x00020000);
+  };
+  auto rsrc_C = [&](const Tile& T) {
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<bf16_t*>(a.C) + (int64_t)T.m0 * a.ldc, (short)0,
+                                             T.rows * a.ldc * 2, 0x00020000);
+  };
+  auto rsrc_B = [&](const Tile& T) {
+    return __builtin_amdgcn_make_buffer_rsrc(
+        a.bias ? const_cast<float*>(a.bias + T.n0) : const_cast<void*>(a.A), (short)0, BN * 4, 0x00020000);
+  };
+  // without a bias the slice lands in a spare region and the bias region
+  // holds zeros (the load count stays the same either way)
+  const int bias_dst = opaque_s(a.bias ? big::BIAS : big::BIAS + 2 * BN);
+  if (!a.bias) reinterpret_cast<float*>(smem + big::BIAS)[tid] = 0.f;
+  auto issue = [&](const Tile& T, int kt, int s) {
+    const uint32_t kb = (uint32_t)kt * BK * 2;
+    const auto rA = rsrc_A(T);
+    const auto rW = rsrc_W(T);
+    bf16_t* la = sA(0) + opaque_s(s * A_STAGE + wave * 64 * BK);
+    bf16_t* lw = sW(0) + opaque_s(s * W_STAGE + wave * 64 * BK);
+    const uint32_t wk = (uint32_t)opaque_s(wave * 64 * K * 2) + kb;
+    const uint32_t ae = (uint32_t)opaque_v((int)a_ev), ao = (uint32_t)opaque_v((int)a_od);
+    const uint32_t a8 = (uint32_t)opaque_s(8 * a.lda * 2);
+#pragma unroll
+    for (int i = 0; i < DMA; ++i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_void_t2*)(la + 8 * i * BK), 16,
+                                               ((i & 1) ? ao : ae) + (uint32_t)i * a8, kb, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, (lds_void_t2*)(lw + 8 * i * BK), 16, (i & 1) ? w_od : w_ev,
+                                               wk + (uint32_t)(8 * i * K * 2), 0, 0);
+    }
+  };
+  // a tile's head: its bias slice (wave w: 64 values) and its first two k-tiles
+  auto issue_head = [&](const Tile& T) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_B(T), (lds_void_t2*)(smem + bias_dst + wave * 128), 4,
+                                             (uint32_t)(wave * 64 + lane) * 4, 0, 0, 0);
+    issue(T, 0, 0);
+    issue(T, 1, 1);
+  };
+
+  f32x16_t acc[FN][FM];
+  // fragment reads: row r = base + frow with base a multiple of 32, so
+  // swz(r, c) = base * BK + swz(frow, c); the lane part is recomputed per
+  // read group (opaque) rather than kept for every stage and step
+  auto load_frags = [&](int s, int st, bf16x8_t(&wf)[FN], bf16x8_t(&xf)[FM]) {
+    const int lo = opaque_v(big::swz(frow, 2 * st + half));
+    const bf16_t* pw = sW(s) + wn * 128 * BK + lo;
+    const bf16_t* pa = sA(s) + wm * 128 * BK + lo;
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+      wf[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(pw + i * 32 * BK));
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+      xf[j] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(pa + j * 32 * BK));
+  };
+  auto mfma_step = [&](const bf16x8_t(&wf)[FN], const bf16x8_t(&xf)[FM]) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], xf[j], acc[i][j], 0, 0, 0);
+  };
+  constexpr int NMF = FN * FM, NRD = FN + FM;
+  bf16x8_t wP[FN], xP[FM], wQ[FN], xQ[FM];
+
+  // one k-tile: steps 0-2 read the next step's fragments while multiplying;
+  // then tile kt + 1 must have landed (the previous tile's stores may still
+  // be in flight in a tile's first k-tile: stores_pending) and every wave be
+  // done with stage s, which is refilled with tile kt + 2 while step 3
+  // multiplies and reads tile kt + 1's first fragments
+  auto k_tile = [&](const Tile& T, int kt, bool stores_pending, auto refill) {
+    const int s = kt & 1;
+    load_frags(s, 1, wQ, xQ);
+    mfma_step(wP, xP);
+    interleave_step<NRD, NMF>();
+    load_frags(s, 2, wP, xP);
+    mfma_step(wQ, xQ);
+    interleave_step<NRD, NMF>();
+    load_frags(s, 3, wQ, xQ);
+    mfma_step(wP, xP);
+    interleave_step<NRD, NMF>();
+    if (stores_pending) big::wait_vm<big::STORES>();
+    else big::wait_vm<0>();
+    lds_barrier();
+    if constexpr (decltype(refill)::value) issue(T, kt + 2, s);
+    // after the last tile these read a stale (in-bounds) stage, never used
+    load_frags(s ^ 1, 0, wP, xP);
+    mfma_step(wQ, xQ);
+    interleave_step<NRD, NMF>();
+  };
+
+  bf16_t* reg = smem + big::RING + wave * big::CHUNK;
+  const int rl = lane >> 3, cl = (lane & 7) * 8;  // read-back: row rl + 8 it, columns cl .. cl + 7
+  int t = blockIdx.x;
+  Tile cur = make_tile(t);
+  issue_head(cur);
+  bool first = true;
+  while (true) {
+    // the tile's bias and k-tile 0 must land (k-tile 1 and the previous
+    // tile's stores may still be in flight)
+    if (first) big::wait_vm<2 * DMA>();
+    else big::wait_vm<2 * DMA + big::STORES>();
+    lds_barrier();
+    const int n_wave = wn * 128;  // within the tile
+    // (the bias slice landed with k-tile 0; read untracked, see lds_read_f4)
+    const float* bl = bias_lds + n_wave + half * 4;
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+      float4 b[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) b[q] = lds_read_f4(bl + i * 32 + q * 8);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      f32x16_t init;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        init[q * 4 + 0] = b[q].x;
+        init[q * 4 + 1] = b[q].y;
+        init[q * 4 + 2] = b[q].z;
+        init[q * 4 + 3] = b[q].w;
+      }
+#pragma unroll
+      for (int j = 0; j < FM; ++j) acc[i][j] = init;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    load_frags(0, 0, wP, xP);
+    int kt = 0;
+    if (KT > 2) k_tile(cur, kt++, !first, std::true_type{});
+    else k_tile(cur, kt++, !first, std::false_type{});
+    for (; kt + 2 < KT; ++kt) k_tile(cur, kt, false, std::true_type{});
+    for (; kt < KT; ++kt) k_tile(cur, kt, false, std::false_type{});
+
+    // the next tile's head loads while this one is written out
+    const int t_next = t + gridDim.x;
+    const bool more = t_next < tiles;
+    Tile nxt;
+    if (more) {
+      nxt = make_tile(t_next);
+      issue_head(nxt);
+    }
+
+    // ---- epilogue: 8 chunks of 32 rows x 64 columns through LDS -------------
+    const auto rC = rsrc_C(cur);
+    const int ldc2 = opaque_s(a.ldc * 2);
+    const uint32_t c_lane = (uint32_t)((wm * 128 + rl) * ldc2 + (cur.n0 + n_wave + cl) * 2);
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+          const int i = 2 * h + ii;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float v0 = acc_read(acc[i][j][q * 4 + 0]), v1 = acc_read(acc[i][j][q * 4 + 1]);
+            float v2 = acc_read(acc[i][j][q * 4 + 2]), v3 = acc_read(acc[i][j][q * 4 + 3]);
+            if constexpr (EPI == EPI_GELU) {
+              round_bf16x2(v0, v1);
+              round_bf16x2(v2, v3);
+              v0 = gelu_tanh_fast(v0);
+              v1 = gelu_tanh_fast(v1);
+              v2 = gelu_tanh_fast(v2);
+              v3 = gelu_tanh_fast(v3);
+            }
+            uint2 p;
+            p.x = pack_bf16x2(v0, v1);
+            p.y = pack_bf16x2(v2, v3);
+            lds_write_b64(reg + frow * EP + ii * 32 + q * 8 + half * 4, p);
+          }
+        }
+        // (LDS operations of one wave run in order: the reads see the writes,
+        // and the next chunk's writes come after these reads)
+        u32x4_t v[4];
+#pragma unroll
+        for (int it = 0; it < 4; ++it) v[it] = lds_read_b128(reg + (it * 8 + rl) * EP + cl);
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3])::"memory");
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+          // row wm 128 + j 32 + it 8 + rl, column n0 + n_wave + h 64 + cl
+          __builtin_amdgcn_raw_buffer_store_b128(v[it], rC, c_lane + (uint32_t)((j * 32 + it * 8) * ldc2 + h * 128),
+                                                 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (!more) break;
+    t = t_next;
+    cur = nxt;
+    first = false;
+  }
+#endif
+}
+
+// ---------------------------------------------------------------------------
 // fp32 GEMM (the fp32 check mode): 64 x 64 tile, BK = 16, 4 x 4 per thread.
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs a) {
@@ -576,8 +922,46 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a) {
   }
 }
 
+// The persistent 256 x 256 kernel takes bf16-weight GEMMs with bf16 output
+// and a store or gelu epilogue whose 256 x 256 tiles fill every CU at least
+// once.
+bool use_big(const GemmArgs& a, int wt, bool f32out) {
+  if (wt != W_BF16 || f32out || a.split > 1 || a.epi == EPI_RESID) return false;
+  if (a.N % big::BN != 0 || a.K % big::BK != 0 || a.K < 2 * big::BK) return false;
+  // buffer offsets inside a tile are 32-bit
+  if ((int64_t)big::BM * a.lda * 2 >= (int64_t)1 << 31 || (int64_t)big::BM * a.ldc * 2 >= (int64_t)1 << 31 ||
+      (int64_t)big::BN * a.K * 2 >= (int64_t)1 << 31)
+    return false;
+  const int64_t tiles = (int64_t)((a.M + big::BM - 1) / big::BM) * (a.N / big::BN);
+  return tiles >= 256;
+}
+
+// compute units of the current device (the persistent grid)
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
 template <int EPI, int WT, bool F32OUT>
 hipError_t launch_mfma(const GemmArgs& a, hipStream_t st) {
+  if constexpr (EPI != EPI_RESID) {
+    if (use_big(a, WT, F32OUT)) {
+      const int tiles = ((a.M + big::BM - 1) / big::BM) * (a.N / big::BN);
+      // a multiple of 8 blocks keeps block b on XCD b % 8 in every round
+      int grid = device_cus() & ~7;
+      grid = grid < 8 ? 8 : grid;
+      grid = tiles < grid ? tiles : grid;
+      hipLaunchKernelGGL(gemm_big_kernel<EPI>, dim3(grid), dim3(256), 0, st, a);
+      return hipGetLastError();
+    }
+  }
   const int num_tm = (a.M + BM - 1) / BM, num_tn = a.N / BN;
   const int tiles = num_tm * num_tn;
   if (a.split > 1) {
@@ -595,6 +979,10 @@ hipError_t launch_mfma(const GemmArgs& a, hipStream_t st) {
 }  // namespace
 
 namespace allie {
+
+bool gemm_uses_persistent(const GemmArgs& a) {
+  return a.M > 0 && (a.epi == EPI_STORE || a.epi == EPI_GELU) && use_big(a, a.wtype, a.out_f32 != 0);
+}
 
 bool gemm_mfma_supported(const GemmArgs& a) {
   return a.N % BN == 0 && a.K % BK == 0 && a.lda % 8 == 0 && a.M > 0;

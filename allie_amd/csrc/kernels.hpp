@@ -58,6 +58,12 @@ struct LNArgs {
   float eps;
   void* y;                 // [rows_out][d] bf16 or fp32
   int act_bf16;
+  // optional residual add before the norm: row src is h[src] + add[src]
+  // (add bf16 [rows][d], bf16 activations only; may alias y, each row is
+  // read whole before it is written), written back to h_out[src] when
+  // h_out is set (may alias h)
+  const void* add;
+  float* h_out;
 };
 hipError_t launch_layernorm(const LNArgs& a, hipStream_t st);
 
@@ -86,6 +92,11 @@ struct GemmArgs {
 };
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t st);
 bool gemm_mfma_supported(const GemmArgs& a);
+// true when this GEMM runs on the persistent 256 x 256 kernel (large M,
+// bf16 weights, store or gelu epilogue); the forward then writes attention
+// and MLP projections with a store epilogue and adds them to the residual
+// stream in the following LayerNorm
+bool gemm_uses_persistent(const GemmArgs& a);
 // K splits the forward uses for an M x N x K MFMA GEMM: enough blocks for
 // every CU when the output tiles alone leave most idle (small M)
 int gemm_split_factor(int M, int N, int K);

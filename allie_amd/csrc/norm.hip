@@ -10,7 +10,9 @@
 // registers already.
 //
 // LayerNorm is GPT-2's (eps 1e-5, affine), statistics in fp32 with the
-// two-pass variance over the register-resident row.  One wave per row; d is a
+// two-pass variance over the register-resident row.  It can first add a bf16
+// GEMM output to the fp32 residual row (h += y, the reference's residual add
+// of a bf16 autocast projection) and write the sum back.  One wave per row; d is a
 // multiple of 256 so each lane owns d/256 float4 groups.
 #include "common.hpp"
 #include "kernels.hpp"
@@ -127,8 +129,21 @@ __global__ __launch_bounds__(256) void layernorm_kernel(allie::LNArgs a) {
   const int64_t src = a.row_idx ? (int64_t)a.row_idx[r] : r;
   float4 v[NV];
 #pragma unroll
-  for (int i = 0; i < NV; ++i)
-    v[i] = *reinterpret_cast<const float4*>(a.h + src * d + (i * 64 + lane) * 4);
+  for (int i = 0; i < NV; ++i) {
+    const int c = (i * 64 + lane) * 4;
+    v[i] = *reinterpret_cast<const float4*>(a.h + src * d + c);
+    if (a.add) {  // h + bf16 GEMM output, in fp32 (exact widening)
+      const uint2 y = *reinterpret_cast<const uint2*>(reinterpret_cast<const bf16_t*>(a.add) + src * d + c);
+      v[i].x += bf2f(y.x & 0xffffu);
+      v[i].y += bf2f(y.x >> 16);
+      v[i].z += bf2f(y.y & 0xffffu);
+      v[i].w += bf2f(y.y >> 16);
+    }
+  }
+  if (a.h_out) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) *reinterpret_cast<float4*>(a.h_out + src * d + (i * 64 + lane) * 4) = v[i];
+  }
   ln_row_store<NV>(v, d, a.g, a.b, a.eps, a.y, r, a.act_bf16);
 }
 
@@ -193,6 +208,7 @@ hipError_t launch_embed_ln(const EmbedArgs& a, hipStream_t st) {
 
 hipError_t launch_layernorm(const LNArgs& a, hipStream_t st) {
   if (a.d % 256 != 0 || a.rows_out < a.rows) return hipErrorInvalidValue;
+  if (a.add && !a.act_bf16) return hipErrorInvalidValue;
   if (a.rows_out == 0) return hipSuccess;
   dim3 grid((a.rows_out + 3) / 4);
   ALLIE_NV_SWITCH(a.d / 256, hipLaunchKernelGGL(layernorm_kernel<NV>, grid, dim3(256), 0, st, a));
