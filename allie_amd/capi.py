@@ -79,7 +79,7 @@ _SIGS = [
     ("allie_gemm_split_factor", C.c_int, [C.c_int, C.c_int, C.c_int]),
     ("allie_attn_varlen", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
-      C.c_float, C.c_void_p, C.c_int, C.c_void_p]),
+      C.c_float, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]),
     ("allie_layernorm", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_float,
       C.c_void_p, C.c_int, C.c_void_p]),

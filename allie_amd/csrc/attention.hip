@@ -5,19 +5,22 @@
 // causal mask, plus key padding at B > 1.  On a packed ragged stream the
 // padding disappears: query i of a game sees keys 0..i of the same game.
 //
-// attn_varlen_bf16_kernel -- one workgroup per (query tile of 64 rows, head),
-// two waves of 32 query rows, key/value tiles of 64 through LDS.  Scores are
-// computed transposed, S^T = K Q^T, with MFMA 32x32x16 bf16, so every lane
-// owns one query (column l % 32) and 16 of the 32 keys of a block: the row
-// max and row sum need one exchange with lane l ^ 32 only.  The output is
-// likewise accumulated transposed, O^T = V^T P^T: P^T is already in the
-// B-operand layout lane by lane (after a fixed permutation of the key index
-// that is applied identically to V^T), and V^T comes from a transposed,
-// padded LDS copy of the value tile.  Online softmax in fp32 with exp2; P
-// enters the PV product as two bf16 MFMA operands, hi = bf16(p) and
-// lo = bf16(p - hi), so the weights keep ~16 mantissa bits (a single bf16 P
-// costs up to 2^-9 relative per weight, enough to flip the bf16 rounding of
-// many attention outputs against an fp32-softmax reference).
+// attn_varlen_seq_kernel -- one workgroup of 8 waves per (game, 4 heads).
+// A head's keys (bf16) and values (converted once to fp16, exact for bf16
+// values in fp16's range) of the whole game are staged in LDS (at most 512
+// tokens, 128 KiB); each wave then takes 32-query tiles in an order that
+// balances the causal work (tile t costs t + 1 key blocks) and waits for
+// the others only when the next head (loaded into registers meanwhile) is
+// staged.  Per 32-key block: S^T = K Q^T with MFMA 32x32x16 bf16, so a
+// lane owns one query and 16 keys (the row max and sum need one exchange
+// with lane l ^ 32); online softmax in fp32 with exp2, the accumulator
+// rescaled only when some lane's running max grows; P goes to fp16 (11
+// significant bits against bf16's 8) and O^T += V^T P^T runs on MFMA
+// 32x32x16 f16, whose V^T fragments come straight from the row-major value
+// rows through gfx950's transposing LDS read (ds_read_b64_tr_b16).
+//
+// Grid: (head group, game), the games in order of decreasing length
+// (seq_order_kernel, a counting sort) so that the longest start first.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -25,146 +28,222 @@ namespace {
 
 using namespace allie;
 
-constexpr int QT = ATTN_Q_TILE;  // 64 query rows per workgroup
-constexpr int KT = 64;           // keys per LDS tile
 constexpr int HD = 64;           // head dim (GPT-2: d_model / n_head = 64)
-constexpr int VT_LD = KT + 4;    // padded row of the transposed value tile
 constexpr int MAX_KEYS_F32 = 512;  // fp32 kernel: keys per query held in LDS
+constexpr int SEQ_WAVES = 8;       // waves per workgroup of the per-game kernel
+constexpr int SEQ_MAXN = 512;      // longest game it stages (max_length)
+constexpr int SEQ_HEADS = 4;       // heads per workgroup (the next one loads during one)
 
-ALLIE_DEV int kswz(int row, int chunk) { return row * HD + ((chunk ^ (row & 7)) << 3); }
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __fp16 fp16x4_ll __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) fp16x4_ll lds_f16x4_t;
 
-__global__ __launch_bounds__(128) void attn_varlen_bf16_kernel(AttnVarlenArgs a) {
-  __shared__ __attribute__((aligned(16))) bf16_t sK[KT * HD];
-  __shared__ __attribute__((aligned(16))) bf16_t sVt[HD * VT_LD];
+// two fp32 -> packed fp16 (round toward zero: exact for bf16 inputs in range)
+ALLIE_DEV uint32_t pk_f16(float a, float b) { return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b)); }
 
-  const int head = blockIdx.x;
-  const int tile = a.tiles[blockIdx.y];
-  const int s = tile >> 5, qt = tile & 31;
+__global__ __launch_bounds__(SEQ_WAVES * 64, 1) void attn_varlen_seq_kernel(AttnVarlenArgs a) {
+  // K rows: 128 B, 16-byte chunk c of row r at c ^ ((r >> 1) & 7) (16
+  // consecutive rows reading one chunk hit distinct bank groups).  V rows
+  // (fp16): 128 B, 8-byte chunk j of row r at j ^ (4 ((r >> 1) & 1)) (the
+  // 4 x 16 blocks the transposing read takes hit distinct bank groups).
+  __shared__ __attribute__((aligned(1024))) uint16_t sK[SEQ_MAXN * HD];
+  __shared__ __attribute__((aligned(1024))) uint16_t sV[SEQ_MAXN * HD];
+
+  const int s = a.order[blockIdx.y];
   const int t0 = a.cu_seqlens[s];
-  const int n = a.cu_seqlens[s + 1] - t0;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = lane >> 5, ql = lane & 31;
-  const int d = a.n_head * HD;
-  const int ld = 3 * d;
+  int n = a.cu_seqlens[s + 1] - t0;
+  if (n <= 0) return;
+  n = n < SEQ_MAXN ? n : SEQ_MAXN;
+  const int npad = (n + 31) & ~31;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int d = a.n_head * HD, ld = 3 * d;
   const bf16_t* __restrict__ qkv = reinterpret_cast<const bf16_t*>(a.qkv);
 
-  // Q fragment (B operand of S^T = K Q^T): query q_pos, hd 16 kk + 8 g .. +7
-  const int q_pos = qt * QT + wave * 32 + ql;
-  bf16x8_t qf[4];
-  {
-    const bool ok = q_pos < n;
-    const bf16_t* qrow = qkv + (int64_t)(t0 + (ok ? q_pos : 0)) * ld + head * HD;
+  // ---- staging of one head's keys and values (rows past n are zero): the
+  // loads of the next head are in flight while this one is computed --------
+  constexpr int PER = SEQ_MAXN * 8 / (SEQ_WAVES * 64);  // 16-byte chunks per thread
+  uint4 kv[PER], vv[PER];
+  auto load_head = [&](int head) {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      u32x4_t v = ok ? *reinterpret_cast<const u32x4_t*>(qrow + kk * 16 + g * 8) : u32x4_t{0, 0, 0, 0};
-      qf[kk] = __builtin_bit_cast(bf16x8_t, v);
+    for (int i = 0; i < PER; ++i) {
+      const int c = tid + i * SEQ_WAVES * 64;
+      const int row = c >> 3, ch = c & 7;
+      kv[i] = make_uint4(0, 0, 0, 0);
+      vv[i] = make_uint4(0, 0, 0, 0);
+      if (row < n) {
+        const bf16_t* src = qkv + (int64_t)(t0 + row) * ld + head * HD + ch * 8;
+        kv[i] = *reinterpret_cast<const uint4*>(src + d);
+        vv[i] = *reinterpret_cast<const uint4*>(src + 2 * d);
+      }
     }
-  }
-  const float sl2 = a.scale * 1.4426950408889634f;  // scale * log2(e)
-  float m_run = -INFINITY, l_run = 0.f;
-  f32x16_t o[2] = {f32x16_t{}, f32x16_t{}};
+  };
+  auto store_head = [&]() {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = tid + i * SEQ_WAVES * 64;
+      const int row = c >> 3, ch = c & 7;
+      if (row >= npad) break;
+      *reinterpret_cast<uint4*>(sK + row * HD + ((ch ^ ((row >> 1) & 7)) << 3)) = kv[i];
+      uint4 h;
+      h.x = pk_f16(bf2f(vv[i].x & 0xffffu), bf2f(vv[i].x >> 16));
+      h.y = pk_f16(bf2f(vv[i].y & 0xffffu), bf2f(vv[i].y >> 16));
+      h.z = pk_f16(bf2f(vv[i].z & 0xffffu), bf2f(vv[i].z >> 16));
+      h.w = pk_f16(bf2f(vv[i].w & 0xffffu), bf2f(vv[i].w >> 16));
+      // 16 bytes = 8-byte chunks 2 ch, 2 ch + 1: the swizzle moves them together
+      *reinterpret_cast<uint4*>(sV + row * HD + ((ch ^ (((row >> 1) & 1) << 1)) << 3)) = h;
+    }
+  };
+  const int h_first = blockIdx.x * SEQ_HEADS;
+  const int h_end = h_first + SEQ_HEADS < a.n_head ? h_first + SEQ_HEADS : a.n_head;
+  load_head(h_first);
+  store_head();
+  __syncthreads();
 
-  const int kv_end = min(n, (qt + 1) * QT);  // keys visible to this tile
-  for (int k0 = 0; k0 < kv_end; k0 += KT) {
-    // ---- stage K (swizzled rows) and V^T (padded) -----------------------
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int cidx = tid + 128 * i;  // 512 chunks: 64 keys x 8 chunks
-      const int key = cidx >> 3, c = cidx & 7;
-      const bool ok = k0 + key < n;
-      const bf16_t* row = qkv + (int64_t)(t0 + k0 + key) * ld + head * HD + c * 8;
-      uint4 kv = ok ? *reinterpret_cast<const uint4*>(row + d) : make_uint4(0, 0, 0, 0);
-      uint4 vv = ok ? *reinterpret_cast<const uint4*>(row + 2 * d) : make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4*>(&sK[kswz(key, c)]) = kv;
-      const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        sVt[(c * 8 + 2 * j) * VT_LD + key] = (bf16_t)(w[j] & 0xffffu);
-        sVt[(c * 8 + 2 * j + 1) * VT_LD + key] = (bf16_t)(w[j] >> 16);
-      }
-    }
-    __syncthreads();
+  const int ql = lane & 31, g = lane >> 5;
+  const float c2 = a.scale * 1.4426950408889634f;  // scale * log2(e)
+  // transposing V read of lane l: row (l % 16) / 4 of a 4-key group, dims
+  // hd0 + 4 (l % 4) .. + 3 with hd0 = 16 ((l / 16) % 2)
+  const int trow = (lane & 15) >> 2;
+  const int tchunk = ((lane >> 4) & 1) * 4 + (lane & 3);  // 8-byte chunk inside a 32-dim block
+  bf16_t* __restrict__ out = reinterpret_cast<bf16_t*>(a.out);
 
-    // ---- S^T for two 32-key blocks ----------------------------------------
-    f32x16_t st[2];
+  auto tile = [&](int head, int qt) {
+    const int q0 = qt * 32;
+    const int qrow = q0 + ql < n ? q0 + ql : n - 1;
+    bf16x8_t qf[4];
+    {
+      const bf16_t* qp = qkv + (int64_t)(t0 + qrow) * ld + head * HD + g * 8;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      st[b] = f32x16_t{};
+      for (int kk = 0; kk < 4; ++kk) qf[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(qp + kk * 16));
+    }
+    float m = -INFINITY, lsum = 0.f;
+    f32x16_t o[2] = {f32x16_t{}, f32x16_t{}};
+    for (int kb = 0; kb <= qt; ++kb) {
+      // ---- S^T = K Q^T for keys kb 32 .. + 31 ---------------------------------
+      f32x16_t st{};
+      {
+        const int krow = kb * 32 + ql;
+        const uint16_t* kr = sK + krow * HD;
+        const int sw = (krow >> 1) & 7;
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int krow = b * 32 + ql;
-        bf16x8_t kf = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(&sK[kswz(krow, kk * 2 + g)]));
-        st[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], st[b], 0, 0, 0);
+        for (int kk = 0; kk < 4; ++kk) {
+          const bf16x8_t kf = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(kr + (((2 * kk + g) ^ sw) << 3)));
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], st, 0, 0, 0);
+        }
+      }
+      // lane holds keys 8 (r / 4) + 4 g + r % 4 of the block for query ql
+      if (kb == qt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (8 * (r >> 2) + 4 * g + (r & 3) > ql) st[r] = -INFINITY;
+      }
+      float mx = st[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, st[r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m, mx);
+      if (__builtin_amdgcn_ballot_w64(m_new > m) != 0) {
+        const float alpha = __builtin_amdgcn_exp2f((m - m_new) * c2);  // m = -inf first: 0
+        lsum *= alpha;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          o[0][r] *= alpha;
+          o[1][r] *= alpha;
+        }
+      }
+      m = m_new;
+      const float mc = m_new * c2;
+      uint32_t pk[8];
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(st[r], c2, -mc));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(st[r + 1], c2, -mc));
+        lsum += p0 + p1;
+        pk[r >> 1] = pk_f16(p0, p1);
+      }
+      // ---- O^T += V^T P^T: k-step mm covers keys 16 mm + {4 g .. 4 g + 3,
+      // 8 + 4 g .. 8 + 4 g + 3} (the S^T layout), identically for V^T -----
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) {
+        const f16x8_t pf = __builtin_bit_cast(f16x8_t, u32x4_t{pk[4 * mm], pk[4 * mm + 1], pk[4 * mm + 2], pk[4 * mm + 3]});
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+          fp16x4_ll lo, hi;
+          {
+            const int r0 = kb * 32 + 16 * mm + 4 * g + trow;  // rows of the two 4-key groups
+            const int r1 = r0 + 8;
+            const int j = hb * 8 + tchunk;
+            lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r0 * HD + ((j ^ (((r0 >> 1) & 1) << 2)) << 2)));
+            hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r1 * HD + ((j ^ (((r1 >> 1) & 1) << 2)) << 2)));
+          }
+          const f16x8_t vf = __builtin_bit_cast(
+              f16x8_t, u32x4_t{__builtin_bit_cast(u32x2_t, lo).x, __builtin_bit_cast(u32x2_t, lo).y,
+                               __builtin_bit_cast(u32x2_t, hi).x, __builtin_bit_cast(u32x2_t, hi).y});
+          o[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[hb], 0, 0, 0);
+        }
       }
     }
-    // ---- mask + online softmax (lane owns query q_pos) -------------------
-    float mx = -INFINITY;
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = k0 + b * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        float v = st[b][r] * sl2;
-        if (key > q_pos || key >= n) v = -INFINITY;
-        st[b][r] = v;
-        mx = fmaxf(mx, v);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = exp2f(m_run - m_new);  // m_run = -inf first: alpha = 0
-    m_run = m_new;
-    float ls = 0.f;
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = exp2f(st[b][r] - m_new);
-        st[b][r] = p;
-        ls += p;
-      }
-    l_run = l_run * alpha + ls;
+    // ---- normalise and store: lane holds dims 32 hb + 8 (r / 4) + 4 g + r % 4
+    if (q0 + ql >= n) return;
+    const float inv = 1.0f / (lsum + __shfl_xor(lsum, 32, 64));
+    bf16_t* orow = out + (int64_t)(t0 + q0 + ql) * d + head * HD;
 #pragma unroll
     for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[hb][r] *= alpha;
-
-    // ---- O^T += V^T P^T --------------------------------------------------
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int mm = 0; mm < 2; ++mm) {
-        // P = P_hi + P_lo, both bf16: the PV product keeps ~16 mantissa bits of
-        // the fp32 probabilities instead of bf16's 8
-        bf16x8_t pf, pl;
-        if (mm == 0) split_bf16x8<0>(st[b], pf, pl); else split_bf16x8<8>(st[b], pf, pl);
-        const int kb = b * 32 + mm * 16 + 4 * g;  // keys kb..kb+3 and kb+8..kb+11
-#pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {
-          const bf16_t* vr = &sVt[(hb * 32 + ql) * VT_LD];
-          u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr + kb);
-          u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + kb + 8);
-          bf16x8_t vf = __builtin_bit_cast(bf16x8_t, u32x4_t{lo.x, lo.y, hi.x, hi.y});
-          o[hb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[hb], 0, 0, 0);
-          o[hb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pl, o[hb], 0, 0, 0);
-        }
+      for (int q4 = 0; q4 < 4; ++q4) {
+        uint2 pv;
+        pv.x = pack_bf16x2(o[hb][q4 * 4 + 0] * inv, o[hb][q4 * 4 + 1] * inv);
+        pv.y = pack_bf16x2(o[hb][q4 * 4 + 2] * inv, o[hb][q4 * 4 + 3] * inv);
+        *reinterpret_cast<uint2*>(orow + hb * 32 + q4 * 8 + 4 * g) = pv;
       }
-  }
-  // ---- normalise and store: lane holds hd 8 (r/4) + 4 g + r%4 of q_pos ----
-  if (q_pos >= n) return;
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  const float inv = 1.0f / l_tot;
-  bf16_t* out = reinterpret_cast<bf16_t*>(a.out) + (int64_t)(t0 + q_pos) * d + head * HD;
-#pragma unroll
-  for (int hb = 0; hb < 2; ++hb)
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int hd = hb * 32 + q4 * 8 + 4 * g;
-      uint2 p;
-      p.x = pack_bf16x2(o[hb][q4 * 4 + 0] * inv, o[hb][q4 * 4 + 1] * inv);
-      p.y = pack_bf16x2(o[hb][q4 * 4 + 2] * inv, o[hb][q4 * 4 + 3] * inv);
-      *reinterpret_cast<uint2*>(out + hd) = p;
+  };
+
+  // per head: 32-query tiles, heaviest first, dealt to the waves in a snake
+  // order; then every wave is done with the staged head and the next one
+  // (loaded meanwhile) takes its place
+  const int T32 = npad / 32;
+  for (int head = h_first; head < h_end; ++head) {
+    const bool more = head + 1 < h_end;
+    if (more) load_head(head + 1);
+    for (int r = 0; r * SEQ_WAVES < T32; ++r) {
+      const int idx = r * SEQ_WAVES + ((r & 1) ? SEQ_WAVES - 1 - wave : wave);
+      if (idx < T32) tile(head, T32 - 1 - idx);
     }
+    if (!more) break;
+    __syncthreads();
+    store_head();
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Games by decreasing length (a counting sort over lengths 0 .. SEQ_MAXN,
+// longer ones clamped; order within a length is arbitrary).  One workgroup.
+constexpr int ORDER_THREADS = 1024;
+__global__ __launch_bounds__(ORDER_THREADS) void seq_order_kernel(const int32_t* __restrict__ cu, int B,
+                                                                  int32_t* __restrict__ order) {
+  __shared__ int bin[SEQ_MAXN + 1];
+  for (int i = threadIdx.x; i <= SEQ_MAXN; i += ORDER_THREADS) bin[i] = 0;
+  __syncthreads();
+  auto len_of = [&](int s) {
+    int n = cu[s + 1] - cu[s];
+    return n < 0 ? 0 : (n > SEQ_MAXN ? SEQ_MAXN : n);
+  };
+  for (int s = threadIdx.x; s < B; s += ORDER_THREADS) atomicAdd(&bin[len_of(s)], 1);
+  __syncthreads();
+  if (threadIdx.x == 0) {  // exclusive scan from the longest length down
+    int acc = 0;
+    for (int l = SEQ_MAXN; l >= 0; --l) {
+      const int c = bin[l];
+      bin[l] = acc;
+      acc += c;
+    }
+  }
+  __syncthreads();
+  for (int s = threadIdx.x; s < B; s += ORDER_THREADS) order[atomicAdd(&bin[len_of(s)], 1)] = s;
 }
 
 // ---------------------------------------------------------------------------
@@ -247,9 +326,12 @@ hipError_t launch_attn_varlen(const AttnVarlenArgs& a, hipStream_t st) {
   // callers guarantee every game has at most MAX_KEYS_F32 tokens (max_length)
   if (a.head_dim != HD) return hipErrorInvalidValue;
   if (a.act_bf16) {
-    if (a.n_tiles == 0) return hipSuccess;
-    if (a.n_tiles > 65535) return hipErrorInvalidValue;  // grid y limit
-    hipLaunchKernelGGL(attn_varlen_bf16_kernel, dim3(a.n_head, a.n_tiles), dim3(128), 0, st, a);
+    if (a.B <= 0) return hipSuccess;
+    if (a.B > 65535 || !a.order) return hipErrorInvalidValue;  // grid y limit; workspace
+    if (!a.order_ready)
+      hipLaunchKernelGGL(seq_order_kernel, dim3(1), dim3(ORDER_THREADS), 0, st, a.cu_seqlens, a.B, a.order);
+    hipLaunchKernelGGL(attn_varlen_seq_kernel, dim3((a.n_head + SEQ_HEADS - 1) / SEQ_HEADS, a.B),
+                       dim3(SEQ_WAVES * 64), 0, st, a);
   } else {
     if (a.T == 0) return hipSuccess;
     hipLaunchKernelGGL(attn_varlen_f32_kernel, dim3((a.T + 3) / 4, a.n_head), dim3(256), 0, st, a);

@@ -185,7 +185,7 @@ size_t part_bytes(const allie_model* m, int T, int heads_rows) {
 
 // Workspace of a prefill of B games / T tokens.
 struct PrefillWS {
-  int32_t *lens, *cu, *ids, *pos, *seq_of, *last, *blk_off, *tiles, *status, *slot;
+  int32_t *lens, *cu, *ids, *pos, *seq_of, *last, *blk_off, *tiles, *status, *slot, *order;
   int64_t* in_off;
   float* h;
   void *x, *qkv, *attn, *ff, *hx;
@@ -213,6 +213,7 @@ PrefillWS layout_prefill(const allie_model* m, int B, int T, char* base) {
   w.last = (int32_t*)take((size_t)B * 4);
   w.blk_off = (int32_t*)take((size_t)(B + 1) * 4);
   w.tiles = (int32_t*)take((size_t)B * max_tiles * 4);
+  w.order = (int32_t*)take((size_t)B * 4);
   w.status = (int32_t*)take(4);
   w.h = (float*)take((size_t)T * d * 4);
   w.x = take((size_t)T * d * a);
@@ -768,6 +769,7 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
   aa.cu_seqlens = w.cu;
   aa.tiles = w.tiles;
   aa.n_tiles = (int)n_tiles;
+  aa.order = w.order;
   aa.B = n_seq;
   aa.T = (int)T;
   aa.n_head = m->H;
@@ -779,8 +781,9 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
   const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff, w.part};
   const void* final_add = nullptr;
   rc = run_layers(m, acts, (int)T, kv_pool ? w.slot : nullptr, kv_pool, kv_pool_blocks,
-                  [&](int) -> int {
+                  [&](int layer) -> int {
                     HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, true, st));
+                    aa.order_ready = layer > 0;  // the game order is computed once per forward
                     HIP_TRY(launch_attn_varlen(aa, st));
                     HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, false, st));
                     return ALLIE_OK;
@@ -1029,8 +1032,8 @@ int allie_gemm_split_factor(int M, int N, int K) { return gemm_split_factor(M, N
 
 int allie_attn_varlen(const void* qkv, const int32_t* cu_seqlens, const int32_t* tiles,
                       int n_tiles, int n_seq, int n_tokens, int n_head, int head_dim,
-                      float scale, void* out, int act_bf16, void* stream) {
-  if (!qkv || !cu_seqlens || !out || (act_bf16 && !tiles) || head_dim != 64 || n_head <= 0)
+                      float scale, void* out, int act_bf16, int32_t* order_ws, void* stream) {
+  if (!qkv || !cu_seqlens || !out || (act_bf16 && !order_ws) || head_dim != 64 || n_head <= 0)
     return fail(ALLIE_ERR_ARG, "bad attention arguments");
   AttnVarlenArgs a{};
   a.qkv = qkv;
@@ -1044,6 +1047,7 @@ int allie_attn_varlen(const void* qkv, const int32_t* cu_seqlens, const int32_t*
   a.scale = scale;
   a.out = out;
   a.act_bf16 = act_bf16;
+  a.order = order_ws;
   HIP_TRY(launch_attn_varlen(a, (hipStream_t)stream));
   return ALLIE_OK;
 }

@@ -108,11 +108,13 @@ int gemm_split_factor(int M, int N, int K);
 struct AttnVarlenArgs {
   const void* qkv;
   const int32_t* cu_seqlens;
-  const int32_t* tiles;  // (seq << 5) | q_tile, heaviest first
+  const int32_t* tiles;  // (seq << 5) | q_tile, heaviest first (unused by the bf16 path)
   int n_tiles, B, T, n_head, head_dim;
   float scale;
   void* out;
   int act_bf16;
+  int32_t* order;        // bf16 path: [B] workspace, games by decreasing length
+  int order_ready;       // order already holds this batch's order (later layers)
 };
 constexpr int ATTN_Q_TILE = 64;
 hipError_t launch_attn_varlen(const AttnVarlenArgs& a, hipStream_t st);

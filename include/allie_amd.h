@@ -219,9 +219,12 @@ int allie_gemm_splitk(const void* A, const void* W, const float* bias, const flo
                       float* R, int M, int N, int K, int epi, int wtype, int out_f32, int split_k,
                       float* part, size_t part_bytes, void* stream);
 int allie_gemm_split_factor(int M, int N, int K);
+/* Varlen causal attention over packed games (qkv [T][3 H 64] -> out [T][H 64]).
+ * bf16: order_ws is device workspace of n_seq int32 (games by length), every
+ * game at most 512 tokens; fp32: tiles/order_ws unused. */
 int allie_attn_varlen(const void* qkv, const int32_t* cu_seqlens, const int32_t* tiles,
                       int n_tiles, int n_seq, int n_tokens, int n_head, int head_dim,
-                      float scale, void* out, int act_bf16, void* stream);
+                      float scale, void* out, int act_bf16, int32_t* order_ws, void* stream);
 int allie_layernorm(const float* h, const int32_t* row_idx, int rows, int rows_out, int d,
                     const float* g, const float* b, float eps, void* y, int act_bf16,
                     void* stream);

@@ -355,8 +355,9 @@ def test_attention_varlen(bf16, H, cuda):
     out = torch.full((T, d), float("nan"), dtype=dt, device=cuda)
     cu_d = torch.from_numpy(cu).to(cuda)
     tiles_d = torch.tensor(tiles, dtype=torch.int32, device=cuda)
+    order_ws = torch.empty(len(lens), dtype=torch.int32, device=cuda)
     rc = L.allie_attn_varlen(capi.ptr(qkv_d), capi.ptr(cu_d), capi.ptr(tiles_d), len(tiles), len(lens), T, H, 64,
-                             0.125, capi.ptr(out), int(bf16), capi.stream_ptr())
+                             0.125, capi.ptr(out), int(bf16), capi.ptr(order_ws), capi.stream_ptr())
     capi.check(rc)
     torch.cuda.synchronize()
     out = out.float().cpu()
