@@ -457,7 +457,13 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
 //
 // k-tiles of 64: every row of a stage is one whole 128-byte line of A or W,
 // so each request fetches a full line.  Two stages (128 KiB): tile kt + 2
-// loads while tiles kt and kt + 1 are multiplied.  The loads are buffer
+// loads while tiles kt and kt + 1 are multiplied, its W rows during k-step 1
+// (a wave reads all four k-steps' W fragments in k-step 0, so after a
+// barrier the stage's W rows are free) and its A rows during k-step 3.
+// Issuing a whole k-tile's 16 loads per wave at one point stalled MFMA issue
+// for ~1300 cycles per k-tile while the texture unit drained them (measured
+// with s_memtime stamps: 3500 cycles per k-tile against 2400 without
+// loads); split in two they hide behind the MFMAs.  The loads are buffer
 // loads straight to LDS over the tile's own rows: rows past M read as 0, the
 // row is in the per-lane offset and the k offset in the scalar one.
 //
@@ -501,6 +507,21 @@ ALLIE_DEV void wait_vm() {
 }  // namespace big
 
 typedef __attribute__((address_space(3))) void lds_void_t2;
+
+// Scheduling hint for a k-step of the persistent kernel: its NM MFMAs with,
+// after the first ones, NR fragment reads, NW LDS writes and (every
+// NM / NV MFMAs) NV loads.
+template <int NR, int NW, int NV, int NM>
+ALLIE_DEV void interleave_rwl() {
+#pragma unroll
+  for (int i = 0; i < NM; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);              // MFMA
+    if (i < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    if (i < NW) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+    if (NV > 0 && i % (NM / (NV > 0 ? NV : 1)) == 0 && i / (NM / (NV > 0 ? NV : 1)) < NV)
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);            // VMEM read
+  }
+}
 
 // The value unchanged, but opaque to the optimizer: keeps address arithmetic
 // inside the tile loop instead of dozens of hoisted registers.
@@ -611,22 +632,31 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
   // holds zeros (the load count stays the same either way)
   const int bias_dst = opaque_s(a.bias ? big::BIAS : big::BIAS + 2 * BN);
   if (!a.bias) reinterpret_cast<float*>(smem + big::BIAS)[tid] = 0.f;
-  auto issue = [&](const Tile& T, int kt, int s) {
+  // DMA of k-tile kt's A rows (issue_a) or W rows (issue_w) into stage s
+  auto issue_a = [&](const Tile& T, int kt, int s) {
     const uint32_t kb = (uint32_t)kt * BK * 2;
     const auto rA = rsrc_A(T);
-    const auto rW = rsrc_W(T);
     bf16_t* la = sA(0) + opaque_s(s * A_STAGE + wave * 64 * BK);
-    bf16_t* lw = sW(0) + opaque_s(s * W_STAGE + wave * 64 * BK);
-    const uint32_t wk = (uint32_t)opaque_s(wave * 64 * K * 2) + kb;
     const uint32_t ae = (uint32_t)opaque_v((int)a_ev), ao = (uint32_t)opaque_v((int)a_od);
     const uint32_t a8 = (uint32_t)opaque_s(8 * a.lda * 2);
 #pragma unroll
-    for (int i = 0; i < DMA; ++i) {
+    for (int i = 0; i < DMA; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_void_t2*)(la + 8 * i * BK), 16,
                                                ((i & 1) ? ao : ae) + (uint32_t)i * a8, kb, 0, 0);
+  };
+  auto issue_w = [&](const Tile& T, int kt, int s) {
+    const uint32_t kb = (uint32_t)kt * BK * 2;
+    const auto rW = rsrc_W(T);
+    bf16_t* lw = sW(0) + opaque_s(s * W_STAGE + wave * 64 * BK);
+    const uint32_t wk = (uint32_t)opaque_s(wave * 64 * K * 2) + kb;
+#pragma unroll
+    for (int i = 0; i < DMA; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, (lds_void_t2*)(lw + 8 * i * BK), 16, (i & 1) ? w_od : w_ev,
                                                wk + (uint32_t)(8 * i * K * 2), 0, 0);
-    }
+  };
+  auto issue = [&](const Tile& T, int kt, int s) {
+    issue_a(T, kt, s);
+    issue_w(T, kt, s);
   };
   // a tile's head: its bias slice (wave w: 64 values) and its first two k-tiles
   auto issue_head = [&](const Tile& T) {
@@ -640,13 +670,14 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
   // fragment reads: row r = base + frow with base a multiple of 32, so
   // swz(r, c) = base * BK + swz(frow, c); the lane part is recomputed per
   // read group (opaque) rather than kept for every stage and step
-  auto load_frags = [&](int s, int st, bf16x8_t(&wf)[FN], bf16x8_t(&xf)[FM]) {
-    const int lo = opaque_v(big::swz(frow, 2 * st + half));
-    const bf16_t* pw = sW(s) + wn * 128 * BK + lo;
-    const bf16_t* pa = sA(s) + wm * 128 * BK + lo;
+  auto load_w = [&](int s, int st, bf16x8_t(&wf)[FN]) {
+    const bf16_t* pw = sW(s) + wn * 128 * BK + opaque_v(big::swz(frow, 2 * st + half));
 #pragma unroll
     for (int i = 0; i < FN; ++i)
       wf[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(pw + i * 32 * BK));
+  };
+  auto load_a = [&](int s, int st, bf16x8_t(&xf)[FM]) {
+    const bf16_t* pa = sA(s) + wm * 128 * BK + opaque_v(big::swz(frow, 2 * st + half));
 #pragma unroll
     for (int j = 0; j < FM; ++j)
       xf[j] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(pa + j * 32 * BK));
@@ -658,33 +689,47 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
       for (int j = 0; j < FM; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], xf[j], acc[i][j], 0, 0, 0);
   };
-  constexpr int NMF = FN * FM, NRD = FN + FM;
-  bf16x8_t wP[FN], xP[FM], wQ[FN], xQ[FM];
+  constexpr int NMF = FN * FM;
+  bf16x8_t w0[FN], w1[FN], w2[FN], w3[FN], xP[FM], xQ[FM];
 
-  // one k-tile: steps 0-2 read the next step's fragments while multiplying;
-  // then tile kt + 1 must have landed (the previous tile's stores may still
-  // be in flight in a tile's first k-tile: stores_pending) and every wave be
-  // done with stage s, which is refilled with tile kt + 2 while step 3
-  // multiplies and reads tile kt + 1's first fragments
-  auto k_tile = [&](const Tile& T, int kt, bool stores_pending, auto refill) {
+  // One k-tile from stage s.  The W fragments of all four k-steps are read in
+  // step 0, so after a barrier the stage's W rows are free and tile kt + 2's
+  // W rows load during step 1; after step 2 tile kt + 1 must have landed
+  // (`newer` loads issued after it may be in flight) and, past a second
+  // barrier, tile kt + 2's A rows load during step 3 while it reads tile
+  // kt + 1's first fragments.  Each burst of loads is half a k-tile's, spread
+  // between MFMAs (a whole k-tile's loads at one point stall MFMA issue
+  // while the texture unit drains them).
+  auto k_tile = [&](const Tile& T, int kt, int newer, auto refill) {
+    constexpr bool RF = decltype(refill)::value;
     const int s = kt & 1;
-    load_frags(s, 1, wQ, xQ);
-    mfma_step(wP, xP);
-    interleave_step<NRD, NMF>();
-    load_frags(s, 2, wP, xP);
-    mfma_step(wQ, xQ);
-    interleave_step<NRD, NMF>();
-    load_frags(s, 3, wQ, xQ);
-    mfma_step(wP, xP);
-    interleave_step<NRD, NMF>();
-    if (stores_pending) big::wait_vm<big::STORES>();
-    else big::wait_vm<0>();
+    load_w(s, 1, w1);
+    load_w(s, 2, w2);
+    load_w(s, 3, w3);
+    load_a(s, 1, xQ);
+    mfma_step(w0, xP);
+    interleave_rwl<16, 0, 0, NMF>();
     lds_barrier();
-    if constexpr (decltype(refill)::value) issue(T, kt + 2, s);
+    if constexpr (RF) issue_w(T, kt + 2, s);
+    load_a(s, 2, xP);
+    mfma_step(w1, xQ);
+    interleave_rwl<FM, 0, RF ? DMA : 0, NMF>();
+    load_a(s, 3, xQ);
+    mfma_step(w2, xP);
+    interleave_rwl<FM, 0, 0, NMF>();
+    switch (newer) {
+      case 0: big::wait_vm<0>(); break;
+      case DMA: big::wait_vm<DMA>(); break;
+      case big::STORES: big::wait_vm<big::STORES>(); break;
+      default: big::wait_vm<DMA + big::STORES>(); break;
+    }
+    lds_barrier();
+    if constexpr (RF) issue_a(T, kt + 2, s);
     // after the last tile these read a stale (in-bounds) stage, never used
-    load_frags(s ^ 1, 0, wP, xP);
-    mfma_step(wQ, xQ);
-    interleave_step<NRD, NMF>();
+    load_w(s ^ 1, 0, w0);
+    load_a(s ^ 1, 0, xP);
+    mfma_step(w3, xQ);
+    interleave_rwl<FN + FM, 0, RF ? DMA : 0, NMF>();
   };
 
   bf16_t* reg = smem + big::RING + wave * big::CHUNK;
@@ -720,12 +765,16 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
       for (int j = 0; j < FM; ++j) acc[i][j] = init;
       __builtin_amdgcn_sched_barrier(0);
     }
-    load_frags(0, 0, wP, xP);
+    load_w(0, 0, w0);
+    load_a(0, 0, xP);
     int kt = 0;
-    if (KT > 2) k_tile(cur, kt++, !first, std::true_type{});
-    else k_tile(cur, kt++, !first, std::false_type{});
-    for (; kt + 2 < KT; ++kt) k_tile(cur, kt, false, std::true_type{});
-    for (; kt < KT; ++kt) k_tile(cur, kt, false, std::false_type{});
+    // newer than tile kt + 1: this k-tile's W refill and, in k-tile 0, the
+    // previous tile's stores
+    const int st0 = first ? 0 : big::STORES;
+    if (KT > 2) k_tile(cur, kt++, DMA + st0, std::true_type{});
+    else k_tile(cur, kt++, st0, std::false_type{});
+    for (; kt + 2 < KT; ++kt) k_tile(cur, kt, DMA, std::true_type{});
+    for (; kt < KT; ++kt) k_tile(cur, kt, 0, std::false_type{});
 
     // the next tile's head loads while this one is written out
     const int t_next = t + gridDim.x;
