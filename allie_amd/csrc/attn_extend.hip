@@ -34,7 +34,6 @@ using namespace allie;
 constexpr int HD = 64;
 constexpr int QT = 64;           // queries per tree-kernel tile
 constexpr int KT = 64;           // prefix keys per LDS tile (4 pool blocks)
-constexpr int VT_LD = KT + 4;    // padded row of the transposed value tile
 constexpr int PREP_THREADS = 1024;
 
 // element offset of (block, layer, k|v, head, offset-in-block, dim 0)
@@ -315,11 +314,20 @@ __global__ __launch_bounds__(256) void attn_extend_wave_kernel(ExtendAttnArgs a)
 }
 
 // ---------------------------------------------------------------------------
-ALLIE_DEV int kswz(int row, int chunk) { return row * HD + ((chunk ^ (row & 7)) << 3); }
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __fp16 fp16x4_ll __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) fp16x4_ll lds_f16x4_t;
+
+// two fp32 -> packed fp16 (round toward zero: exact for bf16 inputs in range)
+ALLIE_DEV uint32_t pk_f16(float a, float b) { return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b)); }
 
 __global__ __launch_bounds__(128) void attn_extend_tree_kernel(ExtendAttnArgs a) {
-  __shared__ __attribute__((aligned(16))) bf16_t sK[KT * HD];
-  __shared__ __attribute__((aligned(16))) bf16_t sVt[HD * VT_LD];
+  // K rows of 128 B: 16-byte chunk c of row r at c ^ ((r >> 1) & 7).  V rows
+  // (converted to fp16) of 128 B: 8-byte chunk j of row r at
+  // j ^ (4 ((r >> 1) & 1)), read transposed (ds_read_b64_tr_b16) as in the
+  // varlen prefill kernel.
+  __shared__ __attribute__((aligned(1024))) uint16_t sK[KT * HD];
+  __shared__ __attribute__((aligned(1024))) uint16_t sV[KT * HD];
 
   const int head = blockIdx.y;
   const int tile = a.tiles[blockIdx.x];
@@ -331,8 +339,12 @@ __global__ __launch_bounds__(128) void attn_extend_tree_kernel(ExtendAttnArgs a)
   const bf16_t* __restrict__ qkv = reinterpret_cast<const bf16_t*>(a.qkv);
   const bf16_t* __restrict__ pool = reinterpret_cast<const bf16_t*>(a.pool);
 
-  const int qi = a.group_start[g] + qt * QT + wave * 32 + ql;
+  const int q_first = a.group_start[g] + qt * QT;
+  const int qi = q_first + wave * 32 + ql;
   const bool q_ok = qi < q_end;
+  // a wave whose 32 queries are all past the group computes nothing (it
+  // still stages its share of the keys)
+  const bool wave_busy = q_first + wave * 32 < q_end;
   bf16x8_t qf[4];  // B operand of S^T = K Q^T: head dims 16 kk + 8 hf .. +7
   {
     const bf16_t* qrow = qkv + (int64_t)(q_ok ? qi : 0) * ld + head * HD;
@@ -342,53 +354,74 @@ __global__ __launch_bounds__(128) void attn_extend_tree_kernel(ExtendAttnArgs a)
       qf[kk] = __builtin_bit_cast(bf16x8_t, v);
     }
   }
-  const float sl2 = a.scale * 1.4426950408889634f;
+  const float c2 = a.scale * 1.4426950408889634f;
   float m_run = -INFINITY, l_run = 0.f;
   f32x16_t o[2] = {f32x16_t{}, f32x16_t{}};
 
-  // ---- phase 1: the group's prefix, 64 keys (4 pool blocks) per LDS tile ----
-  // query qi sees prefix positions below lim (its own position when that is
-  // inside the prefix: the tokens of a new game's prefix)
+  // ---- phase 1: the group's prefix, 64 keys (4 pool blocks) per LDS tile;
+  // the next tile's keys and values load into registers while one is
+  // multiplied.  Query qi sees prefix positions below lim (its own position
+  // when that is inside the prefix: the tokens of a new game's prefix).
   const int P = a.prefix_len[g];
-  const int lim = q_ok ? min(P, a.pos[qi]) : P;
+  const int lim = q_ok ? min(P, a.pos[qi]) : 0;
   const int32_t* btab = a.prefix_blocks + (int64_t)g * a.max_blocks;
-  for (int k0 = 0; k0 < P; k0 += KT) {
-    __syncthreads();
+  // thread's 4 chunks of a tile: key (tid + 128 it) / 8, 16-byte chunk % 8
+  uint4 kv[4], vv[4];
+  auto fetch = [&](int k0) {
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
-      const int cidx = tid + 128 * it;  // 512 chunks: 64 keys x 8 chunks
+      const int cidx = tid + 128 * it;
       const int key = cidx >> 3, c = cidx & 7;
       const int p = k0 + key;
       const int bi = p / KV_BLOCK;
       const int blk = (p < P && bi < a.max_blocks) ? btab[bi] : -1;
-      const bool ok = blk >= 0 && blk < a.pool_blocks;
-      uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-      if (ok) {
+      kv[it] = make_uint4(0, 0, 0, 0);
+      vv[it] = make_uint4(0, 0, 0, 0);
+      if (blk >= 0 && blk < a.pool_blocks) {
         const int64_t base = pool_off(blk, a.n_layer, a.layer, 0, H, head, p % KV_BLOCK) + c * 8;
-        kv = *reinterpret_cast<const uint4*>(pool + base);
-        vv = *reinterpret_cast<const uint4*>(pool + base + (int64_t)H * KV_BLOCK * HD);  // k -> v
-      }
-      *reinterpret_cast<uint4*>(&sK[kswz(key, c)]) = kv;
-      const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        sVt[(c * 8 + 2 * j) * VT_LD + key] = (bf16_t)(w[j] & 0xffffu);
-        sVt[(c * 8 + 2 * j + 1) * VT_LD + key] = (bf16_t)(w[j] >> 16);
+        kv[it] = *reinterpret_cast<const uint4*>(pool + base);
+        vv[it] = *reinterpret_cast<const uint4*>(pool + base + (int64_t)H * KV_BLOCK * HD);  // k -> v
       }
     }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int cidx = tid + 128 * it;
+      const int key = cidx >> 3, c = cidx & 7;
+      *reinterpret_cast<uint4*>(sK + key * HD + ((c ^ ((key >> 1) & 7)) << 3)) = kv[it];
+      uint4 h;
+      h.x = pk_f16(bf2f(vv[it].x & 0xffffu), bf2f(vv[it].x >> 16));
+      h.y = pk_f16(bf2f(vv[it].y & 0xffffu), bf2f(vv[it].y >> 16));
+      h.z = pk_f16(bf2f(vv[it].z & 0xffffu), bf2f(vv[it].z >> 16));
+      h.w = pk_f16(bf2f(vv[it].w & 0xffffu), bf2f(vv[it].w >> 16));
+      *reinterpret_cast<uint4*>(sV + key * HD + ((c ^ (((key >> 1) & 1) << 1)) << 3)) = h;
+    }
+  };
+  // transposing V read of lane l: row (l % 16) / 4 of a 4-key group, dims
+  // 16 ((l / 16) % 2) + 4 (l % 4) .. + 3 of a 32-dim block
+  const int trow = (lane & 15) >> 2;
+  const int tchunk = ((lane >> 4) & 1) * 4 + (lane & 3);
+  if (P > 0) fetch(0);
+  for (int k0 = 0; k0 < P; k0 += KT) {
+    __syncthreads();  // every wave is done with the previous tile
+    stage();
     __syncthreads();
+    if (k0 + KT < P) fetch(k0 + KT);
+    if (!wave_busy) continue;
     f32x16_t st[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       st[b] = f32x16_t{};
+      const int krow = b * 32 + ql;
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        bf16x8_t kf = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(&sK[kswz(b * 32 + ql, kk * 2 + hf)]));
+        const bf16x8_t kf = __builtin_bit_cast(
+            bf16x8_t, *reinterpret_cast<const u32x4_t*>(sK + krow * HD + (((2 * kk + hf) ^ ((krow >> 1) & 7)) << 3)));
         st[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], st[b], 0, 0, 0);
       }
     }
-    // keys past the prefix, at or past the query's position, or in a skipped
-    // block are masked
+    // keys past the query's limit or in a skipped block are masked
     float mx = -INFINITY;
 #pragma unroll
     for (int b = 0; b < 2; ++b)
@@ -397,24 +430,25 @@ __global__ __launch_bounds__(128) void attn_extend_tree_kernel(ExtendAttnArgs a)
         const int p = k0 + b * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
         const int bi = p / KV_BLOCK;
         const int blk = (p < P && bi < a.max_blocks) ? btab[bi] : -1;
-        float v = st[b][r] * sl2;
-        if (blk < 0 || blk >= a.pool_blocks || p >= lim) v = -INFINITY;
-        st[b][r] = v;
-        mx = fmaxf(mx, v);
+        if (blk < 0 || blk >= a.pool_blocks || p >= lim) st[b][r] = -INFINITY;
+        mx = fmaxf(mx, st[b][r]);
       }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m_run, mx);
+    uint32_t pk[2][8];
     if (m_new != -INFINITY) {  // uniform per query (both lanes of a query agree)
-      const float alpha = exp2f(m_run - m_new);
+      const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c2);
       m_run = m_new;
+      const float mc = m_new * c2;
       float ls = 0.f;
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = exp2f(st[b][r] - m_new);
-          st[b][r] = p;
-          ls += p;
+        for (int r = 0; r < 16; r += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(st[b][r], c2, -mc));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(st[b][r + 1], c2, -mc));
+          ls += p0 + p1;
+          pk[b][r >> 1] = pk_f16(p0, p1);
         }
       l_run = l_run * alpha + ls;
 #pragma unroll
@@ -425,23 +459,27 @@ __global__ __launch_bounds__(128) void attn_extend_tree_kernel(ExtendAttnArgs a)
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) st[b][r] = 0.f;
+        for (int r = 0; r < 8; ++r) pk[b][r] = 0u;
     }
+    // O^T += V^T P^T: k-step (b, mm) covers keys 32 b + 16 mm + {4 hf .. +3,
+    // 8 + 4 hf .. +3} (the S^T layout), identically for V^T
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) {
-        bf16x8_t pf, pl;  // P = P_hi + P_lo (see the varlen prefill kernel)
-        if (mm == 0) split_bf16x8<0>(st[b], pf, pl); else split_bf16x8<8>(st[b], pf, pl);
-        const int kb = b * 32 + mm * 16 + 4 * hf;
+        const f16x8_t pf = __builtin_bit_cast(
+            f16x8_t, u32x4_t{pk[b][4 * mm], pk[b][4 * mm + 1], pk[b][4 * mm + 2], pk[b][4 * mm + 3]});
 #pragma unroll
         for (int hb = 0; hb < 2; ++hb) {
-          const bf16_t* vr = &sVt[(hb * 32 + ql) * VT_LD];
-          u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr + kb);
-          u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + kb + 8);
-          bf16x8_t vf = __builtin_bit_cast(bf16x8_t, u32x4_t{lo.x, lo.y, hi.x, hi.y});
-          o[hb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[hb], 0, 0, 0);
-          o[hb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pl, o[hb], 0, 0, 0);
+          const int r0 = b * 32 + 16 * mm + 4 * hf + trow, r1 = r0 + 8;
+          const int j = hb * 8 + tchunk;
+          const fp16x4_ll lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+              (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r0 * HD + ((j ^ (((r0 >> 1) & 1) << 2)) << 2)));
+          const fp16x4_ll hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+              (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r1 * HD + ((j ^ (((r1 >> 1) & 1) << 2)) << 2)));
+          const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
+          const f16x8_t vf = __builtin_bit_cast(f16x8_t, u32x4_t{l2.x, l2.y, h2.x, h2.y});
+          o[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[hb], 0, 0, 0);
         }
       }
   }
@@ -467,10 +505,10 @@ __global__ __launch_bounds__(128) void attn_extend_tree_kernel(ExtendAttnArgs a)
         s = fmaf(bf2f(qw[t] >> 16), bf2f(kw[t] >> 16), s);
       }
     }
-    s = (s + __shfl_xor(s, 32, 64)) * sl2;
+    s = s + __shfl_xor(s, 32, 64);  // raw score, as m_run (scaled in the exponent)
     const float m_new = fmaxf(m_run, s);
-    const float alpha = exp2f(m_run - m_new);
-    const float p = exp2f(s - m_new);
+    const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c2);
+    const float p = __builtin_amdgcn_exp2f((s - m_new) * c2);
     l_run = l_run * alpha + (hf == 0 ? p : 0.f);
     const int64_t vb = kb + (int64_t)H * KV_BLOCK * HD;
 #pragma unroll
