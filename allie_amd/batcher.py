@@ -122,6 +122,8 @@ class ContinuousBatcher:
         self.tokens = 0        # moves appended
         self.keys_read = 0     # keys attended per layer, summed over steps
         self.fed = 0           # tokens fed (moves and new games' prefixes)
+        self.decode_keys = 0   # keys attended by the running games' one-token steps
+        self.decoded = 0       # one-token steps (running games)
         self.record = record
         self.games = [[] for _ in range(n_slots)]
         self.checks = []  # (game so far, predicted next move) when recording
@@ -185,6 +187,8 @@ class ContinuousBatcher:
                 self.games[s] = [int(x) for x in pre[k]]
                 self.checks.append((list(self.games[s]), int(top[last[nR + k]])))
         self.keys_read += int(self.cur[R].sum()) + nR + int((Ps * (Ps + 1) // 2).sum())
+        self.decode_keys += int(self.cur[R].sum()) + nR
+        self.decoded += nR
         self.cur[R] += 1
         for k, s in enumerate(pend):
             self.cur[s] = Ps[k]

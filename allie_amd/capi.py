@@ -20,7 +20,7 @@ W_WTE, W_WPE, W_CTRL, W_LNF_G, W_LNF_B, W_VALUE_W, W_VALUE_B, W_TIME_W, W_TIME_B
  W_PR_B) = range(16, 28)
 
 EPI_STORE, EPI_GELU, EPI_RESID = 0, 1, 2
-PROBE_QKV, PROBE_PROJ, PROBE_FC, PROBE_FC2, PROBE_ATTN = range(5)
+PROBE_QKV, PROBE_PROJ, PROBE_FC, PROBE_FC2, PROBE_ATTN, PROBE_DECODE = range(6)
 WT_BF16, WT_F32, WT_FP8 = 0, 1, 2
 
 

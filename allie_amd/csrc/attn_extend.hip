@@ -538,6 +538,214 @@ __global__ __launch_bounds__(128) void attn_extend_tree_kernel(ExtendAttnArgs a)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Groups of at most 32 tokens sharing a prefix (MCTS children of one node):
+// one workgroup per (group, head) whose W waves take the prefix's 64-key
+// chunks in turn (wave w: chunks w, w + W, ...), so the prefix is read by W
+// chunks at once rather than one tile after another.  A wave holds all of
+// the group's queries (S^T = K Q^T, 32 query columns), loads its chunk's K
+// fragments straight into MFMA registers (a lane's key row is contiguous),
+// stages V as fp16 in its own LDS tile for the transposing read, and keeps
+// its own running max / sum / O.  The waves' partials then merge through LDS
+// and wave w finishes tokens w, w + W, ... (lane = head dim): the private
+// keys (ancestors, then the token itself) and the normalisation.
+constexpr int FAN_CHUNK = 64, FAN_TILE = FAN_CHUNK * HD;  // fp16 V tile = fp32 32 x 64 partial, 8 KiB
+
+ALLIE_DEV void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__global__ __launch_bounds__(512) void attn_extend_fan_kernel(ExtendAttnArgs a, int g0) {
+  extern __shared__ __attribute__((aligned(1024))) uint16_t fan_lds[];
+  const int W = blockDim.x >> 6;
+  const int g = g0 + blockIdx.x, head = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, ql = lane & 31, hf = lane >> 5;
+  uint16_t* sV = fan_lds + wave * FAN_TILE;  // V tile (fp16, rows as in the tree kernel); then O partial
+  float* sML = reinterpret_cast<float*>(fan_lds + W * FAN_TILE);  // [W][m | l][32]
+  const int H = a.n_head, d = H * HD, ld = 3 * d;
+  const bf16_t* __restrict__ qkv = reinterpret_cast<const bf16_t*>(a.qkv);
+  const bf16_t* __restrict__ pool = reinterpret_cast<const bf16_t*>(a.pool);
+  const int i0 = a.group_start[g];
+  const int nq = a.group_start[g + 1] - i0;  // <= 32
+  const int qi = i0 + ql;
+  const bool q_ok = ql < nq;
+  const int P = a.prefix_len[g];
+  const int lim = q_ok ? min(P, a.pos[qi]) : 0;
+  const int32_t* btab = a.prefix_blocks + (int64_t)g * a.max_blocks;
+  auto block_of = [&](int p) {
+    const int bi = p / KV_BLOCK;
+    const int blk = (p < P && bi < a.max_blocks) ? btab[bi] : -1;
+    return (blk >= 0 && blk < a.pool_blocks) ? blk : -1;
+  };
+  const int64_t voff = (int64_t)H * KV_BLOCK * HD;  // k -> v of the same (block, layer, head)
+  bf16x8_t qf[4];  // B operand: head dims 16 kk + 8 hf .. +7 of query ql
+  {
+    const bf16_t* qrow = qkv + (int64_t)(q_ok ? qi : i0) * ld + head * HD + hf * 8;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) qf[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(qrow + kk * 16));
+  }
+  const float c2 = a.scale * 1.4426950408889634f;
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x16_t o[2] = {f32x16_t{}, f32x16_t{}};
+  const int trow = (lane & 15) >> 2;
+  const int tchunk = ((lane >> 4) & 1) * 4 + (lane & 3);
+  const int nch = (max(P, 0) + FAN_CHUNK - 1) / FAN_CHUNK;
+  for (int c = wave; c < nch; c += W) {
+    const int k0 = c * FAN_CHUNK;
+    // loads of the chunk: the V row of key `lane` (8 x 16 bytes), then K
+    // fragments (key 32 b + ql, dims 16 kk + 8 hf .. +7).  A key outside a
+    // valid block reads block 0 and is zeroed (V) or masked (K).
+    const int vblk = block_of(k0 + lane);
+    const uint64_t ok = __ballot(vblk >= 0);  // bit = key - k0
+    uint4 vv[8];
+    {
+      const bf16_t* vr = pool + pool_off(vblk >= 0 ? vblk : 0, a.n_layer, a.layer, 0, H, head, (k0 + lane) % KV_BLOCK) + voff;
+#pragma unroll
+      for (int ch = 0; ch < 8; ++ch) vv[ch] = *reinterpret_cast<const uint4*>(vr + ch * 8);
+    }
+    u32x4_t kf[2][4];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int p = k0 + b * 32 + ql;
+      const int blk = block_of(p);
+      const bf16_t* kr = pool + pool_off(blk >= 0 ? blk : 0, a.n_layer, a.layer, 0, H, head, p % KV_BLOCK) + hf * 8;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) kf[b][kk] = *reinterpret_cast<const u32x4_t*>(kr + kk * 16);
+    }
+    // V row `lane` to the wave's tile as fp16 (8-byte chunk j of row r at
+    // j ^ (4 ((r >> 1) & 1)))
+#pragma unroll
+    for (int ch = 0; ch < 8; ++ch) {
+      const uint4 v = vblk >= 0 ? vv[ch] : make_uint4(0, 0, 0, 0);
+      uint4 h;
+      h.x = pk_f16(bf2f(v.x & 0xffffu), bf2f(v.x >> 16));
+      h.y = pk_f16(bf2f(v.y & 0xffffu), bf2f(v.y >> 16));
+      h.z = pk_f16(bf2f(v.z & 0xffffu), bf2f(v.z >> 16));
+      h.w = pk_f16(bf2f(v.w & 0xffffu), bf2f(v.w >> 16));
+      *reinterpret_cast<uint4*>(sV + lane * HD + ((ch ^ (((lane >> 1) & 1) << 1)) << 3)) = h;
+    }
+    __builtin_amdgcn_sched_barrier(0);  // V registers free before the products
+    f32x16_t st[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      st[b] = f32x16_t{};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        st[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[b][kk]), qf[kk], st[b], 0, 0, 0);
+    }
+    // keys past the query's limit or in a skipped block are masked
+    float mx = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kl = b * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
+        if (k0 + kl >= lim || !((ok >> kl) & 1)) st[b][r] = -INFINITY;
+        mx = fmaxf(mx, st[b][r]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    uint32_t pk[2][8];
+    if (m_new != -INFINITY) {  // uniform per query (both lanes of a query agree)
+      const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c2);
+      m_run = m_new;
+      const float mc = m_new * c2;
+      float ls = 0.f;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(st[b][r], c2, -mc));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(st[b][r + 1], c2, -mc));
+          ls += p0 + p1;
+          pk[b][r >> 1] = pk_f16(p0, p1);
+        }
+      l_run = l_run * alpha + ls;
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[hb][r] *= alpha;
+    } else {
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 8; ++r) pk[b][r] = 0u;
+    }
+    wave_lds_sync();  // the tile's V rows are written
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) {
+        const f16x8_t pf = __builtin_bit_cast(
+            f16x8_t, u32x4_t{pk[b][4 * mm], pk[b][4 * mm + 1], pk[b][4 * mm + 2], pk[b][4 * mm + 3]});
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+          const int r0 = b * 32 + 16 * mm + 4 * hf + trow, r1 = r0 + 8;
+          const int j = hb * 8 + tchunk;
+          const fp16x4_ll lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+              (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r0 * HD + ((j ^ (((r0 >> 1) & 1) << 2)) << 2)));
+          const fp16x4_ll hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+              (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r1 * HD + ((j ^ (((r1 >> 1) & 1) << 2)) << 2)));
+          const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
+          o[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+              __builtin_bit_cast(f16x8_t, u32x4_t{l2.x, l2.y, h2.x, h2.y}), pf, o[hb], 0, 0, 0);
+        }
+      }
+    wave_lds_sync();  // the transposing reads are done before the next tile's writes
+  }
+  // ---- the wave's partial to LDS: O as fp32 [query][64 dims], 16-byte
+  // group j of row q at j ^ (q & 15); running max and sum per query ---------
+  float* so = reinterpret_cast<float*>(sV);
+#pragma unroll
+  for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int j = hb * 8 + q4 * 2 + hf;  // dims 4 j .. 4 j + 3
+      *reinterpret_cast<float4*>(so + ql * HD + ((j ^ (ql & 15)) << 2)) =
+          make_float4(o[hb][q4 * 4 + 0], o[hb][q4 * 4 + 1], o[hb][q4 * 4 + 2], o[hb][q4 * 4 + 3]);
+    }
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  if (hf == 0) {
+    sML[wave * 64 + ql] = m_run;
+    sML[wave * 64 + 32 + ql] = l_tot;
+  }
+  __syncthreads();
+  // ---- wave w finishes tokens w, w + W, ... (lane = head dim) -------------
+  for (int q = wave; q < nq; q += W) {
+    const int i = i0 + q;
+    float m = -INFINITY;
+    for (int w = 0; w < W; ++w) m = fmaxf(m, sML[w * 64 + q]);
+    float l = 0.f, acc = 0.f;
+    for (int w = 0; w < W; ++w) {
+      const float mw = sML[w * 64 + q];
+      if (mw == -INFINITY) continue;
+      const float f = __builtin_amdgcn_exp2f((mw - m) * c2);
+      l += f * sML[w * 64 + 32 + q];
+      acc += f * reinterpret_cast<const float*>(fan_lds + w * FAN_TILE)[q * HD + (((lane >> 2) ^ (q & 15)) << 2) + (lane & 3)];
+    }
+    const float qv = bf2f(qkv[(int64_t)i * ld + head * HD + lane]);
+    int E = a.n_extra[i];
+    E = E < 0 ? 0 : (E > a.max_extra ? a.max_extra : E);
+    for (int e = 0; e < E; ++e) {
+      const int sl = a.extra_slot[(int64_t)i * a.max_extra + e];
+      if (sl < 0 || (sl >> 4) >= a.pool_blocks) continue;
+      const int64_t kb = pool_off(sl >> 4, a.n_layer, a.layer, 0, H, head, sl & 15);
+      const float kv = bf2f(pool[kb + lane]), vv1 = bf2f(pool[kb + voff + lane]);
+      const float sc = wave_sum(qv * kv);  // raw score, as m (scaled in the exponent)
+      const float m_new = fmaxf(m, sc);
+      const float alpha = __builtin_amdgcn_exp2f((m - m_new) * c2);  // m = -inf: 0
+      const float p = __builtin_amdgcn_exp2f((sc - m_new) * c2);
+      l = l * alpha + p;
+      acc = acc * alpha + p * vv1;
+      m = m_new;
+    }
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    reinterpret_cast<bf16_t*>(a.out)[(int64_t)i * d + head * HD + lane] = (bf16_t)f2bf(acc * inv);
+  }
+}
+
 }  // namespace
 
 namespace allie {
@@ -563,6 +771,15 @@ hipError_t launch_attn_extend_wave(const ExtendAttnArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(attn_extend_wave_kernel<bf16_t>, grid, dim3(256), 0, st, a);
   else
     hipLaunchKernelGGL(attn_extend_wave_kernel<float>, grid, dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_extend_fan(const ExtendAttnArgs& a, int g0, hipStream_t st) {
+  if (!a.act_bf16) return hipErrorInvalidValue;
+  const int W = fan_waves(a.max_blocks);
+  const size_t lds = (size_t)W * (FAN_TILE * 2 + 64 * 4);
+  if (a.n_groups > g0)
+    hipLaunchKernelGGL(attn_extend_fan_kernel, dim3(a.n_groups - g0, a.n_head), dim3(64 * W), lds, st, a, g0);
   return hipGetLastError();
 }
 

@@ -820,12 +820,14 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   if (n_groups > (1 << 23)) return fail(ALLIE_ERR_ARG, "too many groups");
   int max_group = 0;
   int n1 = 0;  // leading groups of one token each (decode steps)
+  int max_rest = 0;  // largest group after those
   for (int g = 0; g < n_groups; ++g) {
     const int sz = group_start_host[g + 1] - group_start_host[g];
     if (sz <= 0) return fail(ALLIE_ERR_ARG, "group %d is empty", g);
     if (sz > 64 * 256) return fail(ALLIE_ERR_ARG, "group %d has %d tokens (max 16384)", g, sz);
     max_group = sz > max_group ? sz : max_group;
     if (n1 == g && sz == 1) n1 = g + 1;
+    if (g >= n1) max_rest = sz > max_rest ? sz : max_rest;
   }
   int64_t n_tiles = 0;  // 64-query tiles of the groups after the leading ones
   for (int g = n1; g < n_groups; ++g) n_tiles += (group_start_host[g + 1] - group_start_host[g] + 63) / 64;
@@ -840,7 +842,10 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   // them (decode steps plus new games' prefixes) puts the one-token groups
   // first: those n1 tokens go to the wave kernel, the rest to the tree kernel.
   const bool tree = act && max_group > 1;
-  if (tree) HIP_TRY(launch_extend_tiles(w.group_start, n1, n_groups, w.tiles, st));
+  // groups of at most 32 tokens (MCTS children of one node) take the fan
+  // kernel instead: the waves of a (group, head) split the prefix
+  const bool fan = tree && max_rest <= FAN_MAX_Q;
+  if (tree && !fan) HIP_TRY(launch_extend_tiles(w.group_start, n1, n_groups, w.tiles, st));
 
   ExtendPrepArgs pa{};
   pa.n = n_tok;
@@ -911,11 +916,18 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
                         ExtendAttnArgs wa = xa;
                         wa.n = n1;
                         wa.one_token_groups = 1;
+                        HIP_TRY(probe_mark(ALLIE_PROBE_DECODE, true, st));
                         HIP_TRY(launch_attn_extend_wave(wa, st));
+                        HIP_TRY(probe_mark(ALLIE_PROBE_DECODE, false, st));
                       }
-                      HIP_TRY(launch_attn_extend_tree(xa, st));
+                      if (fan)
+                        HIP_TRY(launch_attn_extend_fan(xa, n1, st));
+                      else
+                        HIP_TRY(launch_attn_extend_tree(xa, st));
                     } else {
+                      HIP_TRY(probe_mark(ALLIE_PROBE_DECODE, true, st));
                       HIP_TRY(launch_attn_extend_wave(xa, st));
+                      HIP_TRY(probe_mark(ALLIE_PROBE_DECODE, false, st));
                     }
                     HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, false, st));
                     return ALLIE_OK;
@@ -926,7 +938,7 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
 }
 
 int allie_probe_begin(int kind, int max_launches) {
-  if (kind < ALLIE_PROBE_QKV || kind > ALLIE_PROBE_ATTN || max_launches <= 0)
+  if (kind < ALLIE_PROBE_QKV || kind > ALLIE_PROBE_DECODE || max_launches <= 0)
     return fail(ALLIE_ERR_ARG, "bad probe arguments");
   for (auto e : g_probe.start) hipEventDestroy(e);
   for (auto e : g_probe.stop) hipEventDestroy(e);

@@ -167,6 +167,15 @@ struct ExtendAttnArgs {
 hipError_t launch_attn_extend_wave(const ExtendAttnArgs& a, hipStream_t st);
 // MFMA tiles of 64 queries sharing a group's prefix (bf16); needs tiles
 hipError_t launch_attn_extend_tree(const ExtendAttnArgs& a, hipStream_t st);
+// Groups g0 .. of at most FAN_MAX_Q tokens each (bf16): one workgroup of
+// fan_waves(max_blocks) waves per (group, head), the waves splitting the
+// prefix's 64-key chunks
+constexpr int FAN_MAX_Q = 32;
+inline int fan_waves(int max_blocks) {
+  const int ch = (max_blocks * KV_BLOCK + 63) / 64;
+  return ch < 1 ? 1 : (ch > 8 ? 8 : ch);
+}
+hipError_t launch_attn_extend_fan(const ExtendAttnArgs& a, int g0, hipStream_t st);
 // tiles[] = (g << 8) | t for every 64-query tile t of every group g in
 // [first_group, n_groups), in order
 hipError_t launch_extend_tiles(const int32_t* group_start, int first_group, int n_groups, int32_t* tiles,

@@ -318,18 +318,18 @@ def bench_c4(args):
     torch.cuda.synchronize()
     assert int(cb.status.item()) == 0, "extend status"
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    probed = min(args.steps, 100)  # attention launches are timed in the first 100 steps
-    probe = Probe(capi.PROBE_ATTN, probed * cfg.n_layer)
-    tok0, keys0, fed0 = cb.tokens, cb.keys_read, 0
-    keys_probed = fed_probed = 0
+    probed = min(args.steps, 100)  # decode attention launches are timed in the first 100 steps
+    probe = Probe(capi.PROBE_DECODE, probed * cfg.n_layer)
+    tok0, keys0 = cb.tokens, cb.keys_read
+    keys_probed = dec_probed = 0
     t0 = time.perf_counter()
     evs[0].record()
     for i in range(args.steps):
-        k_before, f_before = cb.keys_read, cb.fed
+        k_before, d_before = cb.decode_keys, cb.decoded
         cb.step()
         if i < probed:
-            keys_probed += cb.keys_read - k_before
-            fed_probed += cb.fed - f_before
+            keys_probed += cb.decode_keys - k_before
+            dec_probed += cb.decoded - d_before
         evs[i + 1].record()
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
@@ -340,8 +340,9 @@ def bench_c4(args):
     tok_s = appended / el
     d = cfg.d_model
     att_ms = att_tot / max(att_n, 1)
-    # per attention launch (one layer): keys and values read, queries in, outputs out
-    att_bytes = (keys_probed / probed) * 2 * d * 2 + (fed_probed / probed) * 3 * d * 2
+    # per decode-attention launch (one layer): the running games' keys and
+    # values read (all heads), their queries read and outputs written
+    att_bytes = (keys_probed / probed) * 2 * d * 2 + (dec_probed / probed) * 2 * d * 2
     achieved = att_bytes / (att_ms * 1e-3) / 1e9
     res = base_result(args, tok_s, "tokens/s", ms, "bf16",
                       f"C4 continuous-batching self-play decode: medium bf16, {cb.S} slots, prefixes U[1,50], "
@@ -350,7 +351,7 @@ def bench_c4(args):
                       step_ms_p99=float(np.percentile(lat, 99)),
                       mean_keys_per_step=(cb.keys_read - keys0) / args.steps,
                       moves_appended=appended, games_started=cb.games_started)
-    res["roofline"] = {"kernel": "extend attention (decode steps and new games' prefixes over the paged cache)",
+    res["roofline"] = {"kernel": "attn_extend_wave_kernel (decode: one token per running game over its paged KV)",
                        "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": achieved / HBM_PEAK_GBS, "traffic": None, "avg_launch_ms": att_ms,
                        "alg_bytes_per_launch": att_bytes}

@@ -199,7 +199,8 @@ enum {
   ALLIE_PROBE_PROJ,     /* attention output projection GEMM (+ residual) */
   ALLIE_PROBE_FC,       /* MLP c_fc GEMM + gelu */
   ALLIE_PROBE_FC2,      /* MLP c_proj GEMM (+ residual) */
-  ALLIE_PROBE_ATTN      /* varlen causal attention */
+  ALLIE_PROBE_ATTN,     /* attention of a layer (prefill: varlen; extend: all its kernels) */
+  ALLIE_PROBE_DECODE    /* extend: the one-token-group (decode) attention kernel */
 };
 int allie_probe_begin(int kind, int max_launches);
 int allie_probe_end(float* total_ms_host, int* n_launches_host);

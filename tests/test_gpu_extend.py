@@ -69,15 +69,22 @@ def test_decode_steps_match_full_recompute(tiny, mode, tol, cuda):
     eng.close()
 
 
+# (prefix lengths, level-1 children per root): one root of 70 children spans
+# two 64-query tiles of the tree kernel; groups of at most 16 children over
+# prefix tables of at most 8 chunks take the split-prefix kernels in bf16
+# (level 1 of the second case: full, ragged and one-block prefixes, a group of
+# one child after the others), and level 2 of that case (groups of up to 32)
+# the tree kernel again
+TREES = [([37, 64, 100], [3, 70, 5]), ([37, 64, 100, 128, 5], [3, 16, 5, 1, 9])]
+
+
+@pytest.mark.parametrize("prefix,kids", TREES)
 @pytest.mark.parametrize("mode,tol", [("float32", 1e-4), ("bfloat16", 2e-2)])
-def test_tree_levels_match_full_recompute(tiny, mode, tol, cuda):
-    """Roots with shared prefixes; level-1 children (one root has 70, which
-    spans two 64-query tiles) and level-2 grandchildren that see the prefix,
-    their parent and themselves."""
+def test_tree_levels_match_full_recompute(tiny, mode, tol, prefix, kids, cuda):
+    """Roots with shared prefixes; level-1 children and level-2 grandchildren
+    that see the prefix, their parent and themselves."""
     cfg, sd = tiny
     rng = np.random.default_rng(9)
-    prefix = [37, 64, 100]
-    kids = [3, 70, 5]
     R = len(prefix)
     roots = [list(rng.integers(0, 1968, n)) for n in prefix]
     eng = Engine(cfg, sd, mode=mode)
@@ -117,15 +124,18 @@ def test_tree_levels_match_full_recompute(tiny, mode, tol, cuda):
     eng.close()
 
 
+# (tokens of the two new games over extras, tokens of the new game over its own
+# prefix): with 70 the batch takes the tree kernel, with groups of at most 16
+# the split-prefix kernels (a group with an empty prefix among them)
+@pytest.mark.parametrize("new_sizes", [(1, 70, 45), (1, 12, 14)])
 @pytest.mark.parametrize("mode,tol", [("float32", 1e-4), ("bfloat16", 2e-2)])
-def test_mixed_batch_matches_full_recompute(tiny, mode, tol, cuda):
+def test_mixed_batch_matches_full_recompute(tiny, mode, tol, new_sizes, cuda):
     """One extend holding decode steps (one-token groups first), new games'
     whole prefixes and three children sharing a cached game as prefix: the
     batch a continuous batcher runs when games start between decode steps.
     A new game's token t attends tokens 0..t, given either as its extras
-    (prefix_len 0; 1 and 70 tokens, the latter over two query tiles) or as
-    the group's own prefix limited by the token's position (prefix_len 45,
-    one extra: its own slot)."""
+    (prefix_len 0) or as the group's own prefix limited by the token's
+    position (prefix_len = its length, one extra: its own slot)."""
     cfg, sd = tiny
     rng = np.random.default_rng(13)
     B = 6
@@ -140,8 +150,8 @@ def test_mixed_batch_matches_full_recompute(tiny, mode, tol, cuda):
                 kv_block_table=table[:B].contiguous())
     oracle = RefModel(cfg, sd, mode=mode)
     status = torch.zeros(1, dtype=torch.int32, device=cuda)
-    new_pre = [list(rng.integers(0, 1968, 1)), list(rng.integers(0, 1968, 70))]
-    causal_pre = list(rng.integers(0, 1968, 45))
+    new_pre = [list(rng.integers(0, 1968, new_sizes[0])), list(rng.integers(0, 1968, new_sizes[1]))]
+    causal_pre = list(rng.integers(0, 1968, new_sizes[2]))
     kid_ids = rng.integers(0, 1968, 3)
     dec = rng.integers(0, 1968, B)
     ids, pos, sizes, plen, pblk, extra_rows, n_extra, paths = [], [], [], [], [], [], [], []
