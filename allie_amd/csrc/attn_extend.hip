@@ -539,17 +539,45 @@ __global__ __launch_bounds__(128) void attn_extend_tree_kernel(ExtendAttnArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// Groups of at most 32 tokens sharing a prefix (MCTS children of one node):
+// Groups of at most 16 tokens sharing a prefix (MCTS children of one node):
 // one workgroup per (group, head) whose W waves take the prefix's 64-key
-// chunks in turn (wave w: chunks w, w + W, ...), so the prefix is read by W
-// chunks at once rather than one tile after another.  A wave holds all of
-// the group's queries (S^T = K Q^T, 32 query columns), loads its chunk's K
-// fragments straight into MFMA registers (a lane's key row is contiguous),
-// stages V as fp16 in its own LDS tile for the transposing read, and keeps
-// its own running max / sum / O.  The waves' partials then merge through LDS
-// and wave w finishes tokens w, w + W, ... (lane = head dim): the private
-// keys (ancestors, then the token itself) and the normalisation.
-constexpr int FAN_CHUNK = 64, FAN_TILE = FAN_CHUNK * HD;  // fp16 V tile = fp32 32 x 64 partial, 8 KiB
+// chunks in turn (wave w: chunks w, w + W, ...), so a group's whole prefix
+// is requested at once.  A wave holds all of the group's queries in 16x16x32
+// MFMAs (S^T = K Q^T: key rows, query columns), loads its chunk's K
+// fragments straight into MFMA registers (a lane's key row segment is
+// contiguous), stages V as fp16 in its own LDS tile for the transposing
+// read, and keeps its own running max / sum / O.  The waves' partials merge
+// through LDS and wave w finishes tokens w, w + W, ... (lane = head dim):
+// the private keys (ancestors, then the token itself) and the normalisation.
+// Everything a wave needs for its first tokens' private keys is loaded
+// before the prefix loop, so those loads overlap the prefix's.
+constexpr int FAN_CHUNK = 64, FAN_TILE = FAN_CHUNK * HD;  // fp16 V tile (8 KiB); later the fp32 16 x 64 partial
+constexpr int FAN_PT = 2, FAN_PE = 2;  // tokens per wave x private keys per token loaded up front
+__device__ const uint4 fan_zero[64] = {};  // read in place of values outside the prefix
+
+// sum over the wave without LDS instructions (DPP within each row of 16
+// lanes, then the four rows' lane 0), so it needs no wait on outstanding
+// loads into LDS; the result is wave-uniform
+ALLIE_DEV float wave_sum_dpp(float v) {
+  auto dpp = [](float x, int ctrl) -> float {
+    switch (ctrl) {  // the control word must be a constant
+      case 0x140: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x140, 0xf, 0xf, false));
+      case 0x141: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xf, 0xf, false));
+      case 0xb1: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xb1, 0xf, 0xf, false));
+      default: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4e, 0xf, 0xf, false));
+    }
+  };
+  v += dpp(v, 0x140);  // row_mirror: lane i + lane 15 - i
+  v += dpp(v, 0x141);  // row_half_mirror
+  v += dpp(v, 0xb1);   // quad_perm [1, 0, 3, 2]
+  v += dpp(v, 0x4e);   // quad_perm [2, 3, 0, 1]: every lane holds its row's sum
+  const int b = __float_as_int(v);
+  return (__int_as_float(__builtin_amdgcn_readlane(b, 0)) + __int_as_float(__builtin_amdgcn_readlane(b, 16))) +
+         (__int_as_float(__builtin_amdgcn_readlane(b, 32)) + __int_as_float(__builtin_amdgcn_readlane(b, 48)));
+}
+
+// two bf16 (one word) -> two fp16 (exact for bf16 values in fp16's range)
+ALLIE_DEV uint32_t bf16x2_to_f16x2(uint32_t w) { return pk_f16(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u)); }
 
 ALLIE_DEV void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -557,193 +585,254 @@ ALLIE_DEV void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__global__ __launch_bounds__(512) void attn_extend_fan_kernel(ExtendAttnArgs a, int g0) {
+__global__ __launch_bounds__(512, 4) void attn_extend_fan_kernel(ExtendAttnArgs a, int g0) {
   extern __shared__ __attribute__((aligned(1024))) uint16_t fan_lds[];
   const int W = blockDim.x >> 6;
   const int g = g0 + blockIdx.x, head = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, ql = lane & 31, hf = lane >> 5;
-  uint16_t* sV = fan_lds + wave * FAN_TILE;  // V tile (fp16, rows as in the tree kernel); then O partial
-  float* sML = reinterpret_cast<float*>(fan_lds + W * FAN_TILE);  // [W][m | l][32]
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lq = lane & 15, lg = lane >> 4;  // MFMA column (query) and lane group
+  uint16_t* sV = fan_lds + wave * FAN_TILE;
+  float* sML = reinterpret_cast<float*>(fan_lds + W * FAN_TILE);  // [W][m | l][16]
   const int H = a.n_head, d = H * HD, ld = 3 * d;
   const bf16_t* __restrict__ qkv = reinterpret_cast<const bf16_t*>(a.qkv);
   const bf16_t* __restrict__ pool = reinterpret_cast<const bf16_t*>(a.pool);
-  const int i0 = a.group_start[g];
-  const int nq = a.group_start[g + 1] - i0;  // <= 32
-  const int qi = i0 + ql;
-  const bool q_ok = ql < nq;
-  const int P = a.prefix_len[g];
-  const int lim = q_ok ? min(P, a.pos[qi]) : 0;
-  const int32_t* btab = a.prefix_blocks + (int64_t)g * a.max_blocks;
-  auto block_of = [&](int p) {
-    const int bi = p / KV_BLOCK;
-    const int blk = (p < P && bi < a.max_blocks) ? btab[bi] : -1;
-    return (blk >= 0 && blk < a.pool_blocks) ? blk : -1;
-  };
   const int64_t voff = (int64_t)H * KV_BLOCK * HD;  // k -> v of the same (block, layer, head)
-  bf16x8_t qf[4];  // B operand: head dims 16 kk + 8 hf .. +7 of query ql
-  {
-    const bf16_t* qrow = qkv + (int64_t)(q_ok ? qi : i0) * ld + head * HD + hf * 8;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) qf[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(qrow + kk * 16));
-  }
   const float c2 = a.scale * 1.4426950408889634f;
-  float m_run = -INFINITY, l_run = 0.f;
-  f32x16_t o[2] = {f32x16_t{}, f32x16_t{}};
-  const int trow = (lane & 15) >> 2;
-  const int tchunk = ((lane >> 4) & 1) * 4 + (lane & 3);
+  const int i0 = a.group_start[g];
+  const int nq = a.group_start[g + 1] - i0;  // <= 16
+  const int P = a.prefix_len[g];
+  const int32_t* btab = a.prefix_blocks + (int64_t)g * a.max_blocks;
+  // K rows of (block 0, this layer, this head); a block adds bstride
+  const bf16_t* lbase = pool + ((int64_t)a.layer * 2 * H + head) * (KV_BLOCK * HD);
+  const int64_t bstride = (int64_t)a.n_layer * 2 * H * KV_BLOCK * HD;
+  auto slot_ok = [&](int sl) { return sl >= 0 && (sl >> 4) < a.pool_blocks; };
+  auto slot_off = [&](int sl) { return pool_off(slot_ok(sl) ? sl >> 4 : 0, a.n_layer, a.layer, 0, H, head, sl & 15); };
+  auto clamp_e = [&](int E) { return E < 0 ? 0 : (E > a.max_extra ? a.max_extra : E); };
+
+  // ---- the wave's first FAN_PT tokens (w + W t): their first FAN_PE private
+  // keys load together with the prefix and are folded in (lane = head dim)
+  // after it
+  int xn[FAN_PT];
+  float xm[FAN_PT], xl[FAN_PT], xa[FAN_PT];  // running max (raw score), sum, P V
+  uint32_t xq[FAN_PT], xk[FAN_PT][FAN_PE], xv[FAN_PT][FAN_PE];  // raw bf16 (converted where used)
+  int xs[FAN_PT][FAN_PE];
+#pragma unroll
+  for (int t = 0; t < FAN_PT; ++t) {
+    const int q = wave + W * t;
+    const int i = i0 + (q < nq ? q : 0);
+    xn[t] = q < nq ? clamp_e(a.n_extra[i]) : 0;
+#pragma unroll
+    for (int e = 0; e < FAN_PE; ++e) xs[t][e] = e < a.max_extra ? a.extra_slot[(int64_t)i * a.max_extra + e] : -1;
+    xq[t] = qkv[(int64_t)i * ld + head * HD + lane];
+  }
+  auto fold_extras = [&]() {
+#pragma unroll
+    for (int t = 0; t < FAN_PT; ++t) {
+      float m = -INFINITY, l = 0.f, acc = 0.f;
+#pragma unroll
+      for (int e = 0; e < FAN_PE; ++e) {
+        if (e >= xn[t] || !slot_ok(xs[t][e])) continue;  // uniform
+        const float sc = wave_sum_dpp(bf2f(xq[t]) * bf2f(xk[t][e]));  // raw score (scaled in the exponent)
+        const float m_new = fmaxf(m, sc);
+        const float alpha = __builtin_amdgcn_exp2f((m - m_new) * c2);  // m = -inf: 0
+        const float pe = __builtin_amdgcn_exp2f((sc - m_new) * c2);
+        l = l * alpha + pe;
+        acc = acc * alpha + pe * bf2f(xv[t][e]);
+        m = m_new;
+      }
+      xm[t] = m;
+      xl[t] = l;
+      xa[t] = acc;
+    }
+  };
+
   const int nch = (max(P, 0) + FAN_CHUNK - 1) / FAN_CHUNK;
-  for (int c = wave; c < nch; c += W) {
+  // pool block of (chunk c, block b); -1: skipped
+  auto table_entry = [&](int c, int b) {
+    const int bi = c * 4 + b;
+    int v = -1;
+    if (bi < a.max_blocks && bi * KV_BLOCK < P) v = btab[bi];
+    return (v >= 0 && v < a.pool_blocks) ? v : -1;
+  };
+  // lane j holds block j % 4 of the wave's chunk j / 4 (its first 16 chunks)
+  const int bt = table_entry(wave + W * (lane >> 2), lane & 3);
+  // queries: B operand of S^T = K Q^T, query lq, dims 32 ks + 8 lg .. +7
+  const bool q_ok = lq < nq;
+  const int qi = i0 + (q_ok ? lq : 0);
+  const int lim = q_ok ? min(P, a.pos[qi]) : 0;
+  bf16x8_t qf[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+    qf[ks] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(qkv + (int64_t)qi * ld + head * HD + 32 * ks + 8 * lg));
+  // the private keys' rows (their slots are in by now)
+#pragma unroll
+  for (int t = 0; t < FAN_PT; ++t)
+#pragma unroll
+    for (int e = 0; e < FAN_PE; ++e) {
+      const int64_t kb = slot_off(xs[t][e]) + lane;
+      xk[t][e] = pool[kb];
+      xv[t][e] = pool[kb + voff];
+    }
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4_t o[4] = {f32x4_t{}, f32x4_t{}, f32x4_t{}, f32x4_t{}};  // O^T: dims 16 db + 4 lg .. +3 of query lq
+  for (int c = wave, n = 0; c < nch; c += W, ++n) {
     const int k0 = c * FAN_CHUNK;
-    // loads of the chunk: the V row of key `lane` (8 x 16 bytes), then K
-    // fragments (key 32 b + ql, dims 16 kk + 8 hf .. +7).  A key outside a
-    // valid block reads block 0 and is zeroed (V) or masked (K).
-    const int vblk = block_of(k0 + lane);
-    const uint64_t ok = __ballot(vblk >= 0);  // bit = key - k0
-    uint4 vv[8];
+    // the chunk's 4 pool blocks (wave-uniform)
+    int blk[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      blk[b] = __builtin_amdgcn_readfirstlane(n < 16 ? __builtin_amdgcn_readlane(bt, 4 * n + b) : table_entry(c, b));
+    // V rows by DMA: instruction t, lane i fills row r = 8 t + i / 8 at
+    // 16-byte position i % 8 (chunk (i % 8) ^ (2 ((r >> 1) & 1)); the swizzle
+    // bit of r comes from i alone), from block t / 2; rows past the prefix or
+    // in a skipped block read zeros
     {
-      const bf16_t* vr = pool + pool_off(vblk >= 0 ? vblk : 0, a.n_layer, a.layer, 0, H, head, (k0 + lane) % KV_BLOCK) + voff;
+      const int rr = lane >> 3;
+      const int vlo = rr * HD + (((lane & 7) ^ (((rr >> 1) & 1) << 1)) << 3);  // elements
 #pragma unroll
-      for (int ch = 0; ch < 8; ++ch) vv[ch] = *reinterpret_cast<const uint4*>(vr + ch * 8);
+      for (int t = 0; t < 8; ++t) {
+        const int b = t >> 1, r = 8 * t + rr;
+        const bf16_t* vb = lbase + (int64_t)max(blk[b], 0) * bstride + voff + (t & 1) * 8 * HD;
+        const bool vok = blk[b] >= 0 && k0 + r < P;
+        const void* src = vok ? (const void*)(vb + vlo) : (const void*)(reinterpret_cast<const bf16_t*>(fan_zero) + vlo);
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(sV + t * 512), 16, 0, 0);
+      }
     }
-    u32x4_t kf[2][4];
+    // K fragments (key 16 kb + lq, dims 32 ks + 8 lg .. +7) into registers;
+    // keys of a skipped block read block 0 and are masked
+    u32x4_t kf[4][2];
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int p = k0 + b * 32 + ql;
-      const int blk = block_of(p);
-      const bf16_t* kr = pool + pool_off(blk >= 0 ? blk : 0, a.n_layer, a.layer, 0, H, head, p % KV_BLOCK) + hf * 8;
+    for (int kb = 0; kb < 4; ++kb) {
+      const bf16_t* kr = lbase + (int64_t)max(blk[kb], 0) * bstride + lq * HD + 8 * lg;
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) kf[b][kk] = *reinterpret_cast<const u32x4_t*>(kr + kk * 16);
+      for (int ks = 0; ks < 2; ++ks) kf[kb][ks] = *(const __attribute__((address_space(1))) u32x4_t*)(kr + 32 * ks);
     }
-    // V row `lane` to the wave's tile as fp16 (8-byte chunk j of row r at
-    // j ^ (4 ((r >> 1) & 1)))
+    f32x4_t st[4];
 #pragma unroll
-    for (int ch = 0; ch < 8; ++ch) {
-      const uint4 v = vblk >= 0 ? vv[ch] : make_uint4(0, 0, 0, 0);
-      uint4 h;
-      h.x = pk_f16(bf2f(v.x & 0xffffu), bf2f(v.x >> 16));
-      h.y = pk_f16(bf2f(v.y & 0xffffu), bf2f(v.y >> 16));
-      h.z = pk_f16(bf2f(v.z & 0xffffu), bf2f(v.z >> 16));
-      h.w = pk_f16(bf2f(v.w & 0xffffu), bf2f(v.w >> 16));
-      *reinterpret_cast<uint4*>(sV + lane * HD + ((ch ^ (((lane >> 1) & 1) << 1)) << 3)) = h;
+    for (int kb = 0; kb < 4; ++kb) {
+      st[kb] = f32x4_t{};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        st[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[kb][ks]), qf[ks], st[kb], 0, 0, 0);
     }
-    __builtin_amdgcn_sched_barrier(0);  // V registers free before the products
-    f32x16_t st[2];
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      st[b] = f32x16_t{};
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-        st[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[b][kk]), qf[kk], st[b], 0, 0, 0);
-    }
-    // keys past the query's limit or in a skipped block are masked
+    // st[kb][r]: key 16 kb + 4 lg + r of query lq; keys past the query's
+    // limit or in a skipped block are masked
     float mx = -INFINITY;
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kl = b * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-        if (k0 + kl >= lim || !((ok >> kl) & 1)) st[b][r] = -INFINITY;
-        mx = fmaxf(mx, st[b][r]);
+      for (int r = 0; r < 4; ++r) {
+        if (k0 + 16 * kb + 4 * lg + r >= lim || blk[kb] < 0) st[kb][r] = -INFINITY;
+        mx = fmaxf(mx, st[kb][r]);
       }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m_run, mx);
-    uint32_t pk[2][8];
-    if (m_new != -INFINITY) {  // uniform per query (both lanes of a query agree)
+    u32x4_t pf[2];  // P^T of k-step s: keys 32 s + 4 lg + {0..3}, then 32 s + 16 + 4 lg + {0..3}
+    if (m_new != -INFINITY) {  // uniform per query
       const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c2);
       m_run = m_new;
       const float mc = m_new * c2;
+      float p[4][4];
       float ls = 0.f;
 #pragma unroll
-      for (int b = 0; b < 2; ++b)
+      for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; r += 2) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(st[b][r], c2, -mc));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(st[b][r + 1], c2, -mc));
-          ls += p0 + p1;
-          pk[b][r >> 1] = pk_f16(p0, p1);
+        for (int r = 0; r < 4; ++r) {
+          p[kb][r] = __builtin_amdgcn_exp2f(fmaf(st[kb][r], c2, -mc));
+          ls += p[kb][r];
         }
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+        pf[s2] = u32x4_t{pk_f16(p[2 * s2][0], p[2 * s2][1]), pk_f16(p[2 * s2][2], p[2 * s2][3]),
+                         pk_f16(p[2 * s2 + 1][0], p[2 * s2 + 1][1]), pk_f16(p[2 * s2 + 1][2], p[2 * s2 + 1][3])};
       l_run = l_run * alpha + ls;
 #pragma unroll
-      for (int hb = 0; hb < 2; ++hb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[hb][r] *= alpha;
+      for (int db = 0; db < 4; ++db) o[db] *= alpha;
     } else {
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 8; ++r) pk[b][r] = 0u;
+      pf[0] = pf[1] = u32x4_t{0, 0, 0, 0};
     }
-    wave_lds_sync();  // the tile's V rows are written
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the tile's DMA is done
+    wave_lds_sync();
+    // O^T += V^T P^T: A = V^T rows (dims 16 db + lq) in fp16, k-slots as
+    // P^T's, read transposed: lane group lg reads keys 32 s + 4 lg + (lq >> 2)
+    // (and + 16)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-      for (int mm = 0; mm < 2; ++mm) {
-        const f16x8_t pf = __builtin_bit_cast(
-            f16x8_t, u32x4_t{pk[b][4 * mm], pk[b][4 * mm + 1], pk[b][4 * mm + 2], pk[b][4 * mm + 3]});
-#pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {
-          const int r0 = b * 32 + 16 * mm + 4 * hf + trow, r1 = r0 + 8;
-          const int j = hb * 8 + tchunk;
-          const fp16x4_ll lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-              (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r0 * HD + ((j ^ (((r0 >> 1) & 1) << 2)) << 2)));
-          const fp16x4_ll hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-              (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r1 * HD + ((j ^ (((r1 >> 1) & 1) << 2)) << 2)));
-          const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
-          o[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-              __builtin_bit_cast(f16x8_t, u32x4_t{l2.x, l2.y, h2.x, h2.y}), pf, o[hb], 0, 0, 0);
-        }
+      for (int db = 0; db < 4; ++db) {
+        const int r0 = 32 * s2 + 4 * lg + (lq >> 2), r1 = r0 + 16;
+        const int j = 4 * db + (lq & 3);
+        const fp16x4_ll lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r0 * HD + ((j ^ (((r0 >> 1) & 1) << 2)) << 2)));
+        const fp16x4_ll hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r1 * HD + ((j ^ (((r1 >> 1) & 1) << 2)) << 2)));
+        const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
+        const u32x4_t vf{bf16x2_to_f16x2(l2.x), bf16x2_to_f16x2(l2.y), bf16x2_to_f16x2(h2.x), bf16x2_to_f16x2(h2.y)};
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, vf), __builtin_bit_cast(f16x8_t, pf[s2]),
+                                                       o[db], 0, 0, 0);
       }
-    wave_lds_sync();  // the transposing reads are done before the next tile's writes
+    wave_lds_sync();  // the transposing reads are done before the tile is written again
   }
+  fold_extras();  // their loads went out with the prefix's
   // ---- the wave's partial to LDS: O as fp32 [query][64 dims], 16-byte
-  // group j of row q at j ^ (q & 15); running max and sum per query ---------
+  // group j of row q at j ^ q; running max and sum per query -----------------
   float* so = reinterpret_cast<float*>(sV);
 #pragma unroll
-  for (int hb = 0; hb < 2; ++hb)
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int j = hb * 8 + q4 * 2 + hf;  // dims 4 j .. 4 j + 3
-      *reinterpret_cast<float4*>(so + ql * HD + ((j ^ (ql & 15)) << 2)) =
-          make_float4(o[hb][q4 * 4 + 0], o[hb][q4 * 4 + 1], o[hb][q4 * 4 + 2], o[hb][q4 * 4 + 3]);
-    }
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  if (hf == 0) {
-    sML[wave * 64 + ql] = m_run;
-    sML[wave * 64 + 32 + ql] = l_tot;
+  for (int db = 0; db < 4; ++db)
+    *reinterpret_cast<f32x4_t*>(so + lq * HD + (((4 * db + lg) ^ lq) << 2)) = o[db];
+  float l_tot = l_run + __shfl_xor(l_run, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
+  if (lg == 0) {
+    sML[wave * 32 + lq] = m_run;
+    sML[wave * 32 + 16 + lq] = l_tot;
   }
   __syncthreads();
-  // ---- wave w finishes tokens w, w + W, ... (lane = head dim) -------------
-  for (int q = wave; q < nq; q += W) {
+  // ---- wave w finishes tokens w, w + W, ... (lane = head dim): merges the
+  // waves' partials with the token's folded private keys, then its
+  // remaining private keys from e0 on, and normalises -------------------------
+  auto finish = [&](int q, int E, int e0, float m, float l, float acc) {
     const int i = i0 + q;
-    float m = -INFINITY;
-    for (int w = 0; w < W; ++w) m = fmaxf(m, sML[w * 64 + q]);
-    float l = 0.f, acc = 0.f;
-    for (int w = 0; w < W; ++w) {
-      const float mw = sML[w * 64 + q];
-      if (mw == -INFINITY) continue;
-      const float f = __builtin_amdgcn_exp2f((mw - m) * c2);
-      l += f * sML[w * 64 + 32 + q];
-      acc += f * reinterpret_cast<const float*>(fan_lds + w * FAN_TILE)[q * HD + (((lane >> 2) ^ (q & 15)) << 2) + (lane & 3)];
+    float mp = -INFINITY;
+    for (int w = 0; w < W; ++w) mp = fmaxf(mp, sML[w * 32 + q]);
+    if (mp != -INFINITY) {
+      const float mt = fmaxf(m, mp);
+      const float f0 = __builtin_amdgcn_exp2f((m - mt) * c2);  // m = -inf: 0
+      l *= f0;
+      acc *= f0;
+      for (int w = 0; w < W; ++w) {
+        const float mw = sML[w * 32 + q];
+        if (mw == -INFINITY) continue;
+        const float f = __builtin_amdgcn_exp2f((mw - mt) * c2);
+        l += f * sML[w * 32 + 16 + q];
+        acc += f * reinterpret_cast<const float*>(fan_lds + w * FAN_TILE)[q * HD + (((lane >> 2) ^ q) << 2) + (lane & 3)];
+      }
+      m = mt;
     }
-    const float qv = bf2f(qkv[(int64_t)i * ld + head * HD + lane]);
-    int E = a.n_extra[i];
-    E = E < 0 ? 0 : (E > a.max_extra ? a.max_extra : E);
-    for (int e = 0; e < E; ++e) {
-      const int sl = a.extra_slot[(int64_t)i * a.max_extra + e];
-      if (sl < 0 || (sl >> 4) >= a.pool_blocks) continue;
-      const int64_t kb = pool_off(sl >> 4, a.n_layer, a.layer, 0, H, head, sl & 15);
-      const float kv = bf2f(pool[kb + lane]), vv1 = bf2f(pool[kb + voff + lane]);
-      const float sc = wave_sum(qv * kv);  // raw score, as m (scaled in the exponent)
-      const float m_new = fmaxf(m, sc);
-      const float alpha = __builtin_amdgcn_exp2f((m - m_new) * c2);  // m = -inf: 0
-      const float p = __builtin_amdgcn_exp2f((sc - m_new) * c2);
-      l = l * alpha + p;
-      acc = acc * alpha + p * vv1;
-      m = m_new;
+    if (e0 < E) {
+      const float qv = bf2f(qkv[(int64_t)i * ld + head * HD + lane]);
+      for (int e = e0; e < E; ++e) {
+        const int sl = a.extra_slot[(int64_t)i * a.max_extra + e];
+        if (!slot_ok(sl)) continue;
+        const int64_t kb = slot_off(sl) + lane;
+        const float sc = wave_sum(qv * bf2f(pool[kb]));
+        const float m_new = fmaxf(m, sc);
+        const float alpha = __builtin_amdgcn_exp2f((m - m_new) * c2);
+        const float pe = __builtin_amdgcn_exp2f((sc - m_new) * c2);
+        l = l * alpha + pe;
+        acc = acc * alpha + pe * bf2f(pool[kb + voff]);
+        m = m_new;
+      }
     }
     const float inv = l > 0.f ? 1.0f / l : 0.f;
     reinterpret_cast<bf16_t*>(a.out)[(int64_t)i * d + head * HD + lane] = (bf16_t)f2bf(acc * inv);
+  };
+#pragma unroll
+  for (int t = 0; t < FAN_PT; ++t) {
+    const int q = wave + W * t;
+    if (q < nq) finish(q, xn[t], FAN_PE, xm[t], xl[t], xa[t]);
   }
+  for (int q = wave + W * FAN_PT; q < nq; q += W) finish(q, clamp_e(a.n_extra[i0 + q]), 0, -INFINITY, 0.f, 0.f);
 }
 
 }  // namespace
@@ -777,7 +866,7 @@ hipError_t launch_attn_extend_wave(const ExtendAttnArgs& a, hipStream_t st) {
 hipError_t launch_attn_extend_fan(const ExtendAttnArgs& a, int g0, hipStream_t st) {
   if (!a.act_bf16) return hipErrorInvalidValue;
   const int W = fan_waves(a.max_blocks);
-  const size_t lds = (size_t)W * (FAN_TILE * 2 + 64 * 4);
+  const size_t lds = (size_t)W * (FAN_TILE * 2 + 32 * 4);
   if (a.n_groups > g0)
     hipLaunchKernelGGL(attn_extend_fan_kernel, dim3(a.n_groups - g0, a.n_head), dim3(64 * W), lds, st, a, g0);
   return hipGetLastError();

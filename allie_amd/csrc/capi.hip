@@ -842,7 +842,7 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   // them (decode steps plus new games' prefixes) puts the one-token groups
   // first: those n1 tokens go to the wave kernel, the rest to the tree kernel.
   const bool tree = act && max_group > 1;
-  // groups of at most 32 tokens (MCTS children of one node) take the fan
+  // groups of at most 16 tokens (MCTS children of one node) take the fan
   // kernel instead: the waves of a (group, head) split the prefix
   const bool fan = tree && max_rest <= FAN_MAX_Q;
   if (tree && !fan) HIP_TRY(launch_extend_tiles(w.group_start, n1, n_groups, w.tiles, st));

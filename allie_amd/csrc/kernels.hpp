@@ -170,7 +170,7 @@ hipError_t launch_attn_extend_tree(const ExtendAttnArgs& a, hipStream_t st);
 // Groups g0 .. of at most FAN_MAX_Q tokens each (bf16): one workgroup of
 // fan_waves(max_blocks) waves per (group, head), the waves splitting the
 // prefix's 64-key chunks
-constexpr int FAN_MAX_Q = 32;
+constexpr int FAN_MAX_Q = 16;
 inline int fan_waves(int max_blocks) {
   const int ch = (max_blocks * KV_BLOCK + 63) / 64;
   return ch < 1 ? 1 : (ch > 8 ? 8 : ch);
