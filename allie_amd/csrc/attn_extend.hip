@@ -32,7 +32,6 @@ namespace {
 using namespace allie;
 
 constexpr int HD = 64;
-constexpr int QT = 64;           // queries per tree-kernel tile
 constexpr int KT = 64;           // prefix keys per LDS tile (4 pool blocks)
 constexpr int PREP_THREADS = 1024;
 
@@ -76,16 +75,16 @@ __global__ __launch_bounds__(PREP_THREADS) void extend_prepare_kernel(ExtendPrep
   if (threadIdx.x == 0 && a.status) *a.status = (b1 ? 1 : 0) | (b2 ? 2 : 0) | (b4 ? 4 : 0);
 }
 
-// Tile list of the tree kernel: (g << 8) | t for t < ceil(size_g / 64), groups
+// Tile list of the tree kernel: (g << 8) | t for t < ceil(size_g / tq), groups
 // in order.  One workgroup; exclusive scan of the per-group tile counts.
 __global__ __launch_bounds__(PREP_THREADS) void extend_tiles_kernel(const int32_t* __restrict__ group_start,
-                                                                    int g0, int G, int32_t* __restrict__ tiles) {
+                                                                    int g0, int G, int tq, int32_t* __restrict__ tiles) {
   __shared__ int sh[PREP_THREADS / 64 + 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int carry = 0;
   for (int base = g0; base < G; base += PREP_THREADS) {
     const int g = base + threadIdx.x;
-    const int nt = g < G ? (group_start[g + 1] - group_start[g] + QT - 1) / QT : 0;
+    const int nt = g < G ? (group_start[g + 1] - group_start[g] + tq - 1) / tq : 0;
     int x = nt;  // inclusive wave scan
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -321,221 +320,292 @@ typedef __attribute__((address_space(3))) fp16x4_ll lds_f16x4_t;
 // two fp32 -> packed fp16 (round toward zero: exact for bf16 inputs in range)
 ALLIE_DEV uint32_t pk_f16(float a, float b) { return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b)); }
 
-__global__ __launch_bounds__(128) void attn_extend_tree_kernel(ExtendAttnArgs a) {
-  // K rows of 128 B: 16-byte chunk c of row r at c ^ ((r >> 1) & 7).  V rows
-  // (converted to fp16) of 128 B: 8-byte chunk j of row r at
-  // j ^ (4 ((r >> 1) & 1)), read transposed (ds_read_b64_tr_b16) as in the
-  // varlen prefill kernel.
+// Tree kernel: a tile of TQ = 16 NW queries of one group (NW waves of 16
+// queries on 16x16x32 MFMAs) and one head.  Keys arrive in chunks of 64,
+// staged in LDS (K bf16 rows swizzled by kswz; V fp16, 8-byte chunk j of row
+// r at j ^ (4 ((r >> 1) & 1)), read transposed), two chunks loading into registers
+// while one is multiplied.  First the
+// group's prefix (query i sees positions below min(P, pos[i])), then the
+// tile's private keys as columns: for each extra index e, a run of
+// consecutive tokens whose e-th private key is the same pool slot (siblings'
+// common ancestors) is one column, visible to exactly that run of queries.
+// Every (token, e) entry lands in exactly one column, so each query sees each
+// of its private keys once, whatever the slots are.
+constexpr int TREE_EB = 8;  // extra indices per column batch
+// K rows (bf16, 128 B): 16-byte chunk c of row r at c ^ kswz(r)
+ALLIE_DEV int kswz(int r) { return (r >> 1) & 7; }
+
+template <int NW>
+__global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttnArgs a) {
+  constexpr int TQ = NW * 16, NT = NW * 64, PER = 512 / NT;  // PER: 16-byte K (and V) pieces per thread per chunk
+  constexpr int NH = TQ / 64;                               // 64-token halves (column builder waves)
+  constexpr int MAXC = TQ * TREE_EB;
   __shared__ __attribute__((aligned(1024))) uint16_t sK[KT * HD];
   __shared__ __attribute__((aligned(1024))) uint16_t sV[KT * HD];
+  __shared__ int32_t c_slot[MAXC + 64];   // column -> pool slot (-1: padding)
+  __shared__ __attribute__((aligned(16))) uint32_t c_rng[MAXC + 64];  // column -> tile-local queries [lo, hi): lo | hi << 16
+  __shared__ int32_t s_blk[64];           // the prefix's first 64 pool blocks (-1: skipped)
+  __shared__ int32_t s_tot[NH];
 
   const int head = blockIdx.y;
   const int tile = a.tiles[blockIdx.x];
   const int g = tile >> 8, qt = tile & 255;
   const int H = a.n_head, d = H * HD, ld = 3 * d;
-  const int q_end = a.group_start[g + 1];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int hf = lane >> 5, ql = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane & 15, lg = lane >> 4;
   const bf16_t* __restrict__ qkv = reinterpret_cast<const bf16_t*>(a.qkv);
   const bf16_t* __restrict__ pool = reinterpret_cast<const bf16_t*>(a.pool);
-
-  const int q_first = a.group_start[g] + qt * QT;
-  const int qi = q_first + wave * 32 + ql;
-  const bool q_ok = qi < q_end;
-  // a wave whose 32 queries are all past the group computes nothing (it
-  // still stages its share of the keys)
-  const bool wave_busy = q_first + wave * 32 < q_end;
-  bf16x8_t qf[4];  // B operand of S^T = K Q^T: head dims 16 kk + 8 hf .. +7
-  {
-    const bf16_t* qrow = qkv + (int64_t)(q_ok ? qi : 0) * ld + head * HD;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      u32x4_t v = q_ok ? *reinterpret_cast<const u32x4_t*>(qrow + kk * 16 + hf * 8) : u32x4_t{0, 0, 0, 0};
-      qf[kk] = __builtin_bit_cast(bf16x8_t, v);
-    }
-  }
-  const float c2 = a.scale * 1.4426950408889634f;
-  float m_run = -INFINITY, l_run = 0.f;
-  f32x16_t o[2] = {f32x16_t{}, f32x16_t{}};
-
-  // ---- phase 1: the group's prefix, 64 keys (4 pool blocks) per LDS tile;
-  // the next tile's keys and values load into registers while one is
-  // multiplied.  Query qi sees prefix positions below lim (its own position
-  // when that is inside the prefix: the tokens of a new game's prefix).
-  const int P = a.prefix_len[g];
-  const int lim = q_ok ? min(P, a.pos[qi]) : 0;
+  const int64_t voff = (int64_t)H * KV_BLOCK * HD;  // k -> v of the same (block, layer, head)
+  const bf16_t* lbase = pool + ((int64_t)a.layer * 2 * H + head) * (KV_BLOCK * HD);
+  const int64_t bstride = (int64_t)a.n_layer * 2 * H * KV_BLOCK * HD;
+  const int q_first = a.group_start[g] + qt * TQ;
+  const int ntok = min(TQ, a.group_start[g + 1] - q_first);
+  const int P = max(a.prefix_len[g], 0);
   const int32_t* btab = a.prefix_blocks + (int64_t)g * a.max_blocks;
-  // thread's 4 chunks of a tile: key (tid + 128 it) / 8, 16-byte chunk % 8
-  uint4 kv[4], vv[4];
-  auto fetch = [&](int k0) {
+  const int nbp = min((P + KV_BLOCK - 1) / KV_BLOCK, a.max_blocks);  // blocks the prefix reads
+  auto valid_blk = [&](int v) { return (v >= 0 && v < a.pool_blocks) ? v : -1; };
+  auto pblk = [&](int bi) { return bi < 64 ? s_blk[bi] : (bi < nbp ? valid_blk(btab[bi]) : -1); };
+
+  // ---- loads: block table, queries, the private keys' slots --------------
+  if (tid < 64) s_blk[tid] = tid < nbp ? valid_blk(btab[tid]) : -1;
+  const int qloc = wave * 16 + lq;  // tile-local query of this lane
+  const bool q_ok = qloc < ntok;
+  const int qi = q_first + (q_ok ? qloc : 0);
+  const int lim = q_ok ? min(P, a.pos[qi]) : 0;
+  bf16x8_t qf[2];  // B operand of S^T = K Q^T: query lq, dims 32 ks + 8 lg .. +7
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int cidx = tid + 128 * it;
-      const int key = cidx >> 3, c = cidx & 7;
-      const int p = k0 + key;
-      const int bi = p / KV_BLOCK;
-      const int blk = (p < P && bi < a.max_blocks) ? btab[bi] : -1;
-      kv[it] = make_uint4(0, 0, 0, 0);
-      vv[it] = make_uint4(0, 0, 0, 0);
-      if (blk >= 0 && blk < a.pool_blocks) {
-        const int64_t base = pool_off(blk, a.n_layer, a.layer, 0, H, head, p % KV_BLOCK) + c * 8;
-        kv[it] = *reinterpret_cast<const uint4*>(pool + base);
-        vv[it] = *reinterpret_cast<const uint4*>(pool + base + (int64_t)H * KV_BLOCK * HD);  // k -> v
+  for (int ks = 0; ks < 2; ++ks)
+    qf[ks] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(qkv + (int64_t)qi * ld + head * HD + 32 * ks + 8 * lg));
+
+  // columns of extra indices [eb, eb + TREE_EB): wave h < NH builds tokens
+  // 64 h .. 64 h + 63 (lane = token); a run never crosses two halves.  Ends
+  // with the columns, their count in the return value and padding to 64.
+  auto build_columns = [&](int eb) -> int {
+    int sl[TREE_EB];
+    uint64_t M[TREE_EB], brk[TREE_EB];
+    int tot = 0;
+    const int t = wave * 64 + lane;
+    if (wave < NH) {
+      const int i = q_first + t;
+      const bool tv = t < ntok;
+      int E = tv ? a.n_extra[i] : 0;
+      E = E < 0 ? 0 : (E > a.max_extra ? a.max_extra : E);
+#pragma unroll
+      for (int e = 0; e < TREE_EB; ++e) {
+        const int ee = eb + e;
+        const int v = (ee < E) ? a.extra_slot[(int64_t)i * a.max_extra + ee] : -1;
+        sl[e] = (v >= 0 && (v >> 4) < a.pool_blocks) ? v : -1;
+      }
+#pragma unroll
+      for (int e = 0; e < TREE_EB; ++e) {
+        const int prev = __shfl_up(sl[e], 1, 64);
+        const bool start = sl[e] >= 0 && (lane == 0 || prev != sl[e]);
+        M[e] = __ballot(start);
+        brk[e] = M[e] | ~__ballot(sl[e] >= 0);
+        tot += __popcll(M[e]);
+      }
+      if (lane == 0) s_tot[wave] = tot;
+    }
+    __syncthreads();
+    int ncols = 0;
+#pragma unroll
+    for (int h = 0; h < NH; ++h) ncols += s_tot[h];
+    if (wave < NH) {
+      int base = 0;
+      for (int h = 0; h < wave; ++h) base += s_tot[h];
+#pragma unroll
+      for (int e = 0; e < TREE_EB; ++e) {
+        if ((M[e] >> lane) & 1) {
+          const int idx = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(M[e] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)M[e], 0));
+          const uint64_t rest = lane < 63 ? brk[e] >> (lane + 1) : 0;
+          const int hi = rest ? lane + 1 + __builtin_ctzll(rest) : 64;
+          c_slot[idx] = sl[e];
+          c_rng[idx] = (uint32_t)t | ((uint32_t)(wave * 64 + hi) << 16);
+        }
+        base += __popcll(M[e]);
       }
     }
+    if (wave == NW - 1) {  // padding of the last chunk: never visible
+      const int pad = ncols + lane;
+      if (pad < ((ncols + 63) & ~63)) {
+        c_slot[pad] = -1;
+        c_rng[pad] = 0;
+      }
+    }
+    __syncthreads();
+    return ncols;
   };
-  auto stage = [&]() {
+
+  const float c2 = a.scale * 1.4426950408889634f;
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4_t o[4] = {f32x4_t{}, f32x4_t{}, f32x4_t{}, f32x4_t{}};  // O^T: dims 16 db + 4 lg .. +3 of query lq
+  const bool wave_busy = wave * 16 < ntok;  // a wave past the tile's tokens only stages keys
+  const int trow = lq >> 2, tchunk = lq & 3;  // transposing read: key row within 4, 4-dim chunk
+  const int nchp = (P + KT - 1) / KT;
+
+  // chunk j (prefix chunks first, then columns from c_slot) into registers:
+  // this thread's piece it is key row (tid + NT it) / 8, 16-byte chunk % 8;
+  // a key outside a kept block reads block 0 and is zeroed at staging
+  auto fetch = [&](int j, int ncp, uint4 (&kv)[PER], uint4 (&vv)[PER], bool (&okf)[PER]) {
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int cidx = tid + 128 * it;
+    for (int it = 0; it < PER; ++it) {
+      const int cidx = tid + NT * it;
       const int key = cidx >> 3, c = cidx & 7;
-      *reinterpret_cast<uint4*>(sK + key * HD + ((c ^ ((key >> 1) & 7)) << 3)) = kv[it];
+      int blk, off;
+      if (j < ncp) {
+        const int p = j * KT + key;
+        blk = p < P ? pblk(p >> 4) : -1;
+        off = p & 15;
+      } else {
+        const int sl = c_slot[(j - ncp) * 64 + key];
+        blk = sl >= 0 ? sl >> 4 : -1;
+        off = sl & 15;
+      }
+      okf[it] = blk >= 0;
+      const bf16_t* src = lbase + (int64_t)max(blk, 0) * bstride + off * HD + c * 8;
+      kv[it] = *reinterpret_cast<const uint4*>(src);
+      vv[it] = *reinterpret_cast<const uint4*>(src + voff);
+    }
+  };
+  auto stage = [&](const uint4 (&kv)[PER], const uint4 (&vv)[PER], const bool (&okf)[PER]) {
+#pragma unroll
+    for (int it = 0; it < PER; ++it) {
+      const int cidx = tid + NT * it;
+      const int key = cidx >> 3, c = cidx & 7;
+      const uint4 k4 = okf[it] ? kv[it] : make_uint4(0, 0, 0, 0);
+      const uint4 v4 = okf[it] ? vv[it] : make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4*>(sK + key * HD + ((c ^ kswz(key)) << 3)) = k4;
       uint4 h;
-      h.x = pk_f16(bf2f(vv[it].x & 0xffffu), bf2f(vv[it].x >> 16));
-      h.y = pk_f16(bf2f(vv[it].y & 0xffffu), bf2f(vv[it].y >> 16));
-      h.z = pk_f16(bf2f(vv[it].z & 0xffffu), bf2f(vv[it].z >> 16));
-      h.w = pk_f16(bf2f(vv[it].w & 0xffffu), bf2f(vv[it].w >> 16));
+      h.x = pk_f16(bf2f(v4.x & 0xffffu), bf2f(v4.x >> 16));
+      h.y = pk_f16(bf2f(v4.y & 0xffffu), bf2f(v4.y >> 16));
+      h.z = pk_f16(bf2f(v4.z & 0xffffu), bf2f(v4.z >> 16));
+      h.w = pk_f16(bf2f(v4.w & 0xffffu), bf2f(v4.w >> 16));
       *reinterpret_cast<uint4*>(sV + key * HD + ((c ^ (((key >> 1) & 1) << 1)) << 3)) = h;
     }
   };
-  // transposing V read of lane l: row (l % 16) / 4 of a 4-key group, dims
-  // 16 ((l / 16) % 2) + 4 (l % 4) .. + 3 of a 32-dim block
-  const int trow = (lane & 15) >> 2;
-  const int tchunk = ((lane >> 4) & 1) * 4 + (lane & 3);
-  if (P > 0) fetch(0);
-  for (int k0 = 0; k0 < P; k0 += KT) {
-    __syncthreads();  // every wave is done with the previous tile
-    stage();
-    __syncthreads();
-    if (k0 + KT < P) fetch(k0 + KT);
-    if (!wave_busy) continue;
-    f32x16_t st[2];
+  auto compute = [&](int j, int ncp) {
+    // S^T = K Q^T: st[kb][r] is key 16 kb + 4 lg + r of query lq
+    f32x4_t st[4];
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      st[b] = f32x16_t{};
-      const int krow = b * 32 + ql;
+    for (int kb = 0; kb < 4; ++kb) {
+      st[kb] = f32x4_t{};
+      const int row = 16 * kb + lq;
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
+      for (int ks = 0; ks < 2; ++ks) {
         const bf16x8_t kf = __builtin_bit_cast(
-            bf16x8_t, *reinterpret_cast<const u32x4_t*>(sK + krow * HD + (((2 * kk + hf) ^ ((krow >> 1) & 7)) << 3)));
-        st[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], st[b], 0, 0, 0);
+            bf16x8_t, *reinterpret_cast<const u32x4_t*>(sK + row * HD + (((4 * ks + lg) ^ kswz(row)) << 3)));
+        st[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], st[kb], 0, 0, 0);
       }
     }
-    // keys past the query's limit or in a skipped block are masked
+    if (j < ncp) {  // prefix: positions below the query's limit in a kept block
+      const int k0 = j * KT;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const bool bok = pblk((k0 >> 4) + kb) >= 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (!bok || k0 + 16 * kb + 4 * lg + r >= lim) st[kb][r] = -INFINITY;
+      }
+    } else {  // columns: visible to their run of queries
+      const int cb = (j - ncp) * 64;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const uint4 rg = *reinterpret_cast<const uint4*>(c_rng + cb + 16 * kb + 4 * lg);
+        const uint32_t rr[4] = {rg.x, rg.y, rg.z, rg.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (qloc < (int)(rr[r] & 0xffffu) || qloc >= (int)(rr[r] >> 16)) st[kb][r] = -INFINITY;
+      }
+    }
     float mx = -INFINITY;
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int p = k0 + b * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-        const int bi = p / KV_BLOCK;
-        const int blk = (p < P && bi < a.max_blocks) ? btab[bi] : -1;
-        if (blk < 0 || blk >= a.pool_blocks || p >= lim) st[b][r] = -INFINITY;
-        mx = fmaxf(mx, st[b][r]);
-      }
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[kb][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m_run, mx);
-    uint32_t pk[2][8];
-    if (m_new != -INFINITY) {  // uniform per query (both lanes of a query agree)
+    u32x4_t pf[2];  // P^T of k-step s: keys 32 s + 4 lg + {0..3}, then 32 s + 16 + 4 lg + {0..3}
+    if (m_new != -INFINITY) {  // uniform per query
       const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c2);
       m_run = m_new;
       const float mc = m_new * c2;
+      float p[4][4];
       float ls = 0.f;
 #pragma unroll
-      for (int b = 0; b < 2; ++b)
+      for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; r += 2) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(st[b][r], c2, -mc));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(st[b][r + 1], c2, -mc));
-          ls += p0 + p1;
-          pk[b][r >> 1] = pk_f16(p0, p1);
+        for (int r = 0; r < 4; ++r) {
+          p[kb][r] = __builtin_amdgcn_exp2f(fmaf(st[kb][r], c2, -mc));
+          ls += p[kb][r];
         }
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+        pf[s2] = u32x4_t{pk_f16(p[2 * s2][0], p[2 * s2][1]), pk_f16(p[2 * s2][2], p[2 * s2][3]),
+                         pk_f16(p[2 * s2 + 1][0], p[2 * s2 + 1][1]), pk_f16(p[2 * s2 + 1][2], p[2 * s2 + 1][3])};
       l_run = l_run * alpha + ls;
 #pragma unroll
-      for (int hb = 0; hb < 2; ++hb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[hb][r] *= alpha;
+      for (int db = 0; db < 4; ++db) o[db] *= alpha;
     } else {
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 8; ++r) pk[b][r] = 0u;
+      pf[0] = pf[1] = u32x4_t{0, 0, 0, 0};
     }
-    // O^T += V^T P^T: k-step (b, mm) covers keys 32 b + 16 mm + {4 hf .. +3,
-    // 8 + 4 hf .. +3} (the S^T layout), identically for V^T
+    // O^T += V^T P^T: A = V^T rows (dims 16 db + lq), k-slots as P^T's;
+    // lane group lg reads keys 32 s + 4 lg + trow (and + 16) transposed
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-      for (int mm = 0; mm < 2; ++mm) {
-        const f16x8_t pf = __builtin_bit_cast(
-            f16x8_t, u32x4_t{pk[b][4 * mm], pk[b][4 * mm + 1], pk[b][4 * mm + 2], pk[b][4 * mm + 3]});
-#pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {
-          const int r0 = b * 32 + 16 * mm + 4 * hf + trow, r1 = r0 + 8;
-          const int j = hb * 8 + tchunk;
-          const fp16x4_ll lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-              (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r0 * HD + ((j ^ (((r0 >> 1) & 1) << 2)) << 2)));
-          const fp16x4_ll hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-              (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r1 * HD + ((j ^ (((r1 >> 1) & 1) << 2)) << 2)));
-          const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
-          const f16x8_t vf = __builtin_bit_cast(f16x8_t, u32x4_t{l2.x, l2.y, h2.x, h2.y});
-          o[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[hb], 0, 0, 0);
-        }
+      for (int db = 0; db < 4; ++db) {
+        const int r0 = 32 * s2 + 4 * lg + trow, r1 = r0 + 16;
+        const int jj = 4 * db + tchunk;
+        const fp16x4_ll lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r0 * HD + ((jj ^ (((r0 >> 1) & 1) << 2)) << 2)));
+        const fp16x4_ll hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r1 * HD + ((jj ^ (((r1 >> 1) & 1) << 2)) << 2)));
+        const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, u32x4_t{l2.x, l2.y, h2.x, h2.y}),
+                                                       __builtin_bit_cast(f16x8_t, pf[s2]), o[db], 0, 0, 0);
       }
+  };
+
+  // two chunks in flight: chunk j + 2 loads into the registers chunk j was
+  // staged from while j is multiplied
+  uint4 kA[PER], vA[PER], kB[PER], vB[PER];
+  bool oA[PER], oB[PER];
+  __syncthreads();  // s_blk is in
+  if (nchp > 0) fetch(0, nchp, kA, vA, oA);  // the prefix's first chunks load while the columns are built
+  if (nchp > 1) fetch(1, nchp, kB, vB, oB);
+  for (int eb = 0; eb < a.max_extra || eb == 0; eb += TREE_EB) {
+    const int ncols = build_columns(eb);
+    const int ncp = eb == 0 ? nchp : 0;  // prefix chunks go with the first batch
+    const int nch = ncp + (ncols + 63) / 64;
+    if (ncp < 1 && nch > 0) fetch(0, ncp, kA, vA, oA);
+    if (ncp < 2 && nch > 1) fetch(1, ncp, kB, vB, oB);
+    for (int j = 0; j < nch; j += 2) {
+      __syncthreads();  // every wave is done with the previous chunk
+      stage(kA, vA, oA);
+      __syncthreads();
+      if (j + 2 < nch) fetch(j + 2, ncp, kA, vA, oA);
+      if (wave_busy) compute(j, ncp);
+      if (j + 1 >= nch) break;
+      __syncthreads();
+      stage(kB, vB, oB);
+      __syncthreads();
+      if (j + 3 < nch) fetch(j + 3, ncp, kB, vB, oB);
+      if (wave_busy) compute(j + 1, ncp);
+    }
   }
   if (!q_ok) return;  // no barriers below
-
-  // ---- phase 2: the query's private keys (ancestors, then itself) -----------
-  // lanes l and l ^ 32 share query qi: each holds half of q (dims 16 kk + 8 hf
-  // + [0, 8)) and half of o (dims 32 hb + 8 q4 + 4 hf + [0, 4)).
-  int E = a.n_extra[qi];
-  E = E < 0 ? 0 : (E > a.max_extra ? a.max_extra : E);
-  for (int e = 0; e < E; ++e) {
-    const int sl = a.extra_slot[(int64_t)qi * a.max_extra + e];
-    if (sl < 0 || (sl >> 4) >= a.pool_blocks) continue;  // same decision in both lanes
-    const int64_t kb = pool_off(sl >> 4, a.n_layer, a.layer, 0, H, head, sl & 15);
-    float s = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const u32x4_t kw = *reinterpret_cast<const u32x4_t*>(pool + kb + kk * 16 + hf * 8);
-      const u32x4_t qw = __builtin_bit_cast(u32x4_t, qf[kk]);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        s = fmaf(bf2f(qw[t] & 0xffffu), bf2f(kw[t] & 0xffffu), s);
-        s = fmaf(bf2f(qw[t] >> 16), bf2f(kw[t] >> 16), s);
-      }
-    }
-    s = s + __shfl_xor(s, 32, 64);  // raw score, as m_run (scaled in the exponent)
-    const float m_new = fmaxf(m_run, s);
-    const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c2);
-    const float p = __builtin_amdgcn_exp2f((s - m_new) * c2);
-    l_run = l_run * alpha + (hf == 0 ? p : 0.f);
-    const int64_t vb = kb + (int64_t)H * KV_BLOCK * HD;
-#pragma unroll
-    for (int hb = 0; hb < 2; ++hb)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const u32x2_t vw = *reinterpret_cast<const u32x2_t*>(pool + vb + hb * 32 + q4 * 8 + 4 * hf);
-        o[hb][q4 * 4 + 0] = o[hb][q4 * 4 + 0] * alpha + p * bf2f(vw.x & 0xffffu);
-        o[hb][q4 * 4 + 1] = o[hb][q4 * 4 + 1] * alpha + p * bf2f(vw.x >> 16);
-        o[hb][q4 * 4 + 2] = o[hb][q4 * 4 + 2] * alpha + p * bf2f(vw.y & 0xffffu);
-        o[hb][q4 * 4 + 3] = o[hb][q4 * 4 + 3] * alpha + p * bf2f(vw.y >> 16);
-      }
-    m_run = m_new;
-  }
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  float l_tot = l_run + __shfl_xor(l_run, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  bf16_t* out = reinterpret_cast<bf16_t*>(a.out) + (int64_t)qi * d + head * HD;
+  bf16_t* out = reinterpret_cast<bf16_t*>(a.out) + (int64_t)qi * d + head * HD + 4 * lg;
 #pragma unroll
-  for (int hb = 0; hb < 2; ++hb)
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int hd = hb * 32 + q4 * 8 + 4 * hf;
-      uint2 p;
-      p.x = pack_bf16x2(o[hb][q4 * 4 + 0] * inv, o[hb][q4 * 4 + 1] * inv);
-      p.y = pack_bf16x2(o[hb][q4 * 4 + 2] * inv, o[hb][q4 * 4 + 3] * inv);
-      *reinterpret_cast<uint2*>(out + hd) = p;
-    }
+  for (int db = 0; db < 4; ++db) {
+    uint2 w;
+    w.x = pack_bf16x2(o[db][0] * inv, o[db][1] * inv);
+    w.y = pack_bf16x2(o[db][2] * inv, o[db][3] * inv);
+    *reinterpret_cast<uint2*>(out + 16 * db) = w;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -844,11 +914,12 @@ hipError_t launch_extend_prepare(const ExtendPrepArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-hipError_t launch_extend_tiles(const int32_t* group_start, int first_group, int n_groups, int32_t* tiles,
+hipError_t launch_extend_tiles(const int32_t* group_start, int first_group, int n_groups, int tile_q, int32_t* tiles,
                                hipStream_t st) {
   if (first_group >= n_groups) return hipSuccess;
+  if (tile_q <= 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(extend_tiles_kernel, dim3(1), dim3(PREP_THREADS), 0, st, group_start, first_group, n_groups,
-                     tiles);
+                     tile_q, tiles);
   return hipGetLastError();
 }
 
@@ -875,7 +946,8 @@ hipError_t launch_attn_extend_fan(const ExtendAttnArgs& a, int g0, hipStream_t s
 hipError_t launch_attn_extend_tree(const ExtendAttnArgs& a, hipStream_t st) {
   if (!a.act_bf16 || a.tiles == nullptr) return hipErrorInvalidValue;
   if (a.n_tiles == 0) return hipSuccess;
-  hipLaunchKernelGGL(attn_extend_tree_kernel, dim3(a.n_tiles, a.n_head), dim3(128), 0, st, a);
+  if (a.tile_q != TREE_TQ) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(attn_extend_tree_kernel<TREE_TQ / 16>, dim3(a.n_tiles, a.n_head), dim3(TREE_TQ * 4), 0, st, a);
   return hipGetLastError();
 }
 

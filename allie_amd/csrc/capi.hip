@@ -814,7 +814,7 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   if (!out->value || !out->time || !out->top1 || !out->max_logit || !out->lse)
     return fail(ALLIE_ERR_ARG, "value/time/top1/max_logit/lse outputs are required");
   if (legal && legal_words * 32 < 1968) return fail(ALLIE_ERR_ARG, "legal mask too narrow");
-  // groups: contiguous, non-empty, covering [0, n_tok); tiles of 64 queries
+  // groups: contiguous, non-empty, covering [0, n_tok)
   if (group_start_host[0] != 0 || group_start_host[n_groups] != n_tok)
     return fail(ALLIE_ERR_ARG, "group_start must run from 0 to n_tok");
   if (n_groups > (1 << 23)) return fail(ALLIE_ERR_ARG, "too many groups");
@@ -829,15 +829,17 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
     if (n1 == g && sz == 1) n1 = g + 1;
     if (g >= n1) max_rest = sz > max_rest ? sz : max_rest;
   }
-  int64_t n_tiles = 0;  // 64-query tiles of the groups after the leading ones
-  for (int g = n1; g < n_groups; ++g) n_tiles += (group_start_host[g + 1] - group_start_host[g] + 63) / 64;
+  const int tile_q = TREE_TQ;  // queries per tree-kernel tile
+  int64_t n_tiles = 0;
+  for (int g = n1; g < n_groups; ++g)
+    n_tiles += (group_start_host[g + 1] - group_start_host[g] + tile_q - 1) / tile_q;
   ExtendWS w = layout_extend(m, n_tok, n_groups, (char*)workspace);
   if (workspace_bytes < w.total)
     return fail(ALLIE_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, w.total);
   hipStream_t st = (hipStream_t)stream;
   const int act = m->act_bf16;
   if ((rc = upload_i32(m, w.group_start, group_start_host, (size_t)n_groups + 1, st))) return rc;
-  // the tree kernel shares a group's prefix across a 64-query tile; groups of
+  // the tree kernel shares a group's prefix across a tile of queries; groups of
   // one token (decode) stream it with one wave per query.  A batch that mixes
   // them (decode steps plus new games' prefixes) puts the one-token groups
   // first: those n1 tokens go to the wave kernel, the rest to the tree kernel.
@@ -845,7 +847,7 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   // groups of at most 16 tokens (MCTS children of one node) take the fan
   // kernel instead: the waves of a (group, head) split the prefix
   const bool fan = tree && max_rest <= FAN_MAX_Q;
-  if (tree && !fan) HIP_TRY(launch_extend_tiles(w.group_start, n1, n_groups, w.tiles, st));
+  if (tree && !fan) HIP_TRY(launch_extend_tiles(w.group_start, n1, n_groups, tile_q, w.tiles, st));
 
   ExtendPrepArgs pa{};
   pa.n = n_tok;
@@ -898,6 +900,7 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   xa.max_extra = max_extra;
   xa.tiles = w.tiles;
   xa.n_tiles = (int)n_tiles;
+  xa.tile_q = tile_q;
   xa.pool = kv_pool;
   xa.pool_blocks = kv_pool_blocks;
   xa.n_layer = m->L;

@@ -155,8 +155,8 @@ struct ExtendAttnArgs {
   const int32_t* extra_slot;   // [n][max_extra]
   const int32_t* n_extra;      // [n]
   int max_extra;
-  const int32_t* tiles;        // MFMA kernel: (group << 8) | q_tile of 64 queries
-  int n_tiles;
+  const int32_t* tiles;        // tree kernel: (group << 8) | q_tile of tile_q queries
+  int n_tiles, tile_q;         // tile_q: TREE_TQ
   const void* pool;            // pool base (the kernel adds the layer offset)
   int pool_blocks, n_layer, layer;
   float scale;
@@ -165,7 +165,9 @@ struct ExtendAttnArgs {
 };
 // one wave per (token, head), any group sizes, bf16 or fp32
 hipError_t launch_attn_extend_wave(const ExtendAttnArgs& a, hipStream_t st);
-// MFMA tiles of 64 queries sharing a group's prefix (bf16); needs tiles
+// MFMA tiles of TREE_TQ queries sharing a group's prefix, private keys as
+// columns (bf16); needs tiles
+constexpr int TREE_TQ = 128;
 hipError_t launch_attn_extend_tree(const ExtendAttnArgs& a, hipStream_t st);
 // Groups g0 .. of at most FAN_MAX_Q tokens each (bf16): one workgroup of
 // fan_waves(max_blocks) waves per (group, head), the waves splitting the
@@ -176,9 +178,9 @@ inline int fan_waves(int max_blocks) {
   return ch < 1 ? 1 : (ch > 8 ? 8 : ch);
 }
 hipError_t launch_attn_extend_fan(const ExtendAttnArgs& a, int g0, hipStream_t st);
-// tiles[] = (g << 8) | t for every 64-query tile t of every group g in
+// tiles[] = (g << 8) | t for every tile_q-query tile t of every group g in
 // [first_group, n_groups), in order
-hipError_t launch_extend_tiles(const int32_t* group_start, int first_group, int n_groups, int32_t* tiles,
+hipError_t launch_extend_tiles(const int32_t* group_start, int first_group, int n_groups, int tile_q, int32_t* tiles,
                                hipStream_t st);
 
 // Validates an extend batch and derives each token's own pool slot (the last
