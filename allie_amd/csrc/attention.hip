@@ -330,8 +330,8 @@ hipError_t launch_attn_varlen(const AttnVarlenArgs& a, hipStream_t st) {
     if (a.B > 65535 || !a.order) return hipErrorInvalidValue;  // grid y limit; workspace
     if (!a.order_ready)
       hipLaunchKernelGGL(seq_order_kernel, dim3(1), dim3(ORDER_THREADS), 0, st, a.cu_seqlens, a.B, a.order);
-    hipLaunchKernelGGL(attn_varlen_seq_kernel, dim3((a.n_head + SEQ_HEADS - 1) / SEQ_HEADS, a.B),
-                       dim3(SEQ_WAVES * 64), 0, st, a);
+    launch_timed(attn_varlen_seq_kernel, dim3((a.n_head + SEQ_HEADS - 1) / SEQ_HEADS, a.B), dim3(SEQ_WAVES * 64), 0,
+                 st, a);
   } else {
     if (a.T == 0) return hipSuccess;
     hipLaunchKernelGGL(attn_varlen_f32_kernel, dim3((a.T + 3) / 4, a.n_head), dim3(256), 0, st, a);

@@ -168,12 +168,47 @@ ALLIE_DEV void widen16(const Row16<T>& r, float (&v)[16]) {
   }
 }
 
+// Order of the decode tokens (one-token groups 0 .. n - 1) for the wave
+// kernel: most keys first, so the longest games do not start last.  One
+// workgroup, a counting sort over 64 bins of 16 keys (order within a bin is
+// arbitrary; every token's result is independent of it).
+constexpr int ORDER_BINS = 64;
+__global__ __launch_bounds__(PREP_THREADS) void decode_order_kernel(ExtendAttnArgs a, int n, int32_t* __restrict__ order) {
+  __shared__ int bin[ORDER_BINS];
+  if (threadIdx.x < ORDER_BINS) bin[threadIdx.x] = 0;
+  __syncthreads();
+  auto bin_of = [&](int i) {
+    int E = a.n_extra[i];
+    E = E < 0 ? 0 : (E > a.max_extra ? a.max_extra : E);
+    const int keys = max(min(a.prefix_len[i], a.pos[i]), 0) + E;
+    return ORDER_BINS - 1 - min(keys / KV_BLOCK, ORDER_BINS - 1);  // bin 0: the most keys
+  };
+  for (int i = threadIdx.x; i < n; i += PREP_THREADS) atomicAdd(&bin[bin_of(i)], 1);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int b = 0; b < ORDER_BINS; ++b) {
+      const int c = bin[b];
+      bin[b] = acc;
+      acc += c;
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < n; i += PREP_THREADS) order[atomicAdd(&bin[bin_of(i)], 1)] = i;
+}
+
+template <int CTRL>
+ALLIE_DEV float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+ALLIE_DEV float readlane_f(float x, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)); }
+
 template <typename T>
 __global__ __launch_bounds__(256) void attn_extend_wave_kernel(ExtendAttnArgs a) {
   const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int H = a.n_head, d = H * HD;
   if (wid >= (int64_t)a.n * H) return;  // no barriers below: whole waves leave
-  const int i = (int)(wid / H), head = (int)(wid % H);
+  const int i = a.order ? a.order[wid / H] : (int)(wid / H), head = (int)(wid % H);
   const int lane = threadIdx.x & 63;
   const int kj = lane >> 2, dq = (lane & 3) * 16;
   // group of token i: group_start[g] <= i < group_start[g + 1]
@@ -252,12 +287,15 @@ __global__ __launch_bounds__(256) void attn_extend_wave_kernel(ExtendAttnArgs a)
 #pragma unroll
       for (int j = 0; j < 16; ++j) s = fmaf(q[j], kv[j], s);
     }
-    s += __shfl_xor(s, 1, 64);  // the 4 lanes of a key share ok
-    s += __shfl_xor(s, 2, 64);
+    // cross-lane steps by DPP and lane reads, no LDS round trips: the 4 lanes
+    // of a key (which share ok) sum their dims, then the max over the row's 4
+    // keys and the 4 rows' maxima
+    s += dpp_f<0xb1>(s);  // quad_perm [1, 0, 3, 2]
+    s += dpp_f<0x4e>(s);  // quad_perm [2, 3, 0, 1]
     s = ok ? s : -INFINITY;
-    float mb = s;
-#pragma unroll
-    for (int o = 4; o < 64; o <<= 1) mb = fmaxf(mb, __shfl_xor(mb, o, 64));
+    float mb = fmaxf(s, dpp_f<0x124>(s));  // row_ror 4
+    mb = fmaxf(mb, dpp_f<0x128>(mb));       // row_ror 8
+    mb = fmaxf(fmaxf(readlane_f(mb, 0), readlane_f(mb, 16)), fmaxf(readlane_f(mb, 32), readlane_f(mb, 48)));
     const float m_new = fmaxf(m_run, mb);
     if (m_new == -INFINITY) return;  // nothing visible yet (wave-uniform)
     const float alpha = exp2f(m_run - m_new);
@@ -923,23 +961,29 @@ hipError_t launch_extend_tiles(const int32_t* group_start, int first_group, int 
   return hipGetLastError();
 }
 
+hipError_t launch_decode_order(const ExtendAttnArgs& a, int n, int32_t* order, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  if (!order) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(decode_order_kernel, dim3(1), dim3(PREP_THREADS), 0, st, a, n, order);
+  return hipGetLastError();
+}
+
 hipError_t launch_attn_extend_wave(const ExtendAttnArgs& a, hipStream_t st) {
   const int64_t waves = (int64_t)a.n * a.n_head;
   if (waves == 0) return hipSuccess;
   const dim3 grid((unsigned)((waves + 3) / 4));
   if (a.act_bf16)
-    hipLaunchKernelGGL(attn_extend_wave_kernel<bf16_t>, grid, dim3(256), 0, st, a);
+    launch_timed(attn_extend_wave_kernel<bf16_t>, grid, dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL(attn_extend_wave_kernel<float>, grid, dim3(256), 0, st, a);
+    launch_timed(attn_extend_wave_kernel<float>, grid, dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
-hipError_t launch_attn_extend_fan(const ExtendAttnArgs& a, int g0, hipStream_t st) {
-  if (!a.act_bf16) return hipErrorInvalidValue;
-  const int W = fan_waves(a.max_blocks);
+hipError_t launch_attn_extend_fan(const ExtendAttnArgs& a, int g0, int g1, int waves, hipStream_t st) {
+  if (!a.act_bf16 || g1 > a.n_groups || waves > 8) return hipErrorInvalidValue;
+  const int W = waves > 0 ? waves : fan_waves(a.max_blocks);
   const size_t lds = (size_t)W * (FAN_TILE * 2 + 32 * 4);
-  if (a.n_groups > g0)
-    hipLaunchKernelGGL(attn_extend_fan_kernel, dim3(a.n_groups - g0, a.n_head), dim3(64 * W), lds, st, a, g0);
+  if (g1 > g0) launch_timed(attn_extend_fan_kernel, dim3(g1 - g0, a.n_head), dim3(64 * W), (uint32_t)lds, st, a, g0);
   return hipGetLastError();
 }
 
@@ -947,7 +991,7 @@ hipError_t launch_attn_extend_tree(const ExtendAttnArgs& a, hipStream_t st) {
   if (!a.act_bf16 || a.tiles == nullptr) return hipErrorInvalidValue;
   if (a.n_tiles == 0) return hipSuccess;
   if (a.tile_q != TREE_TQ) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(attn_extend_tree_kernel<TREE_TQ / 16>, dim3(a.n_tiles, a.n_head), dim3(TREE_TQ * 4), 0, st, a);
+  launch_timed(attn_extend_tree_kernel<TREE_TQ / 16>, dim3(a.n_tiles, a.n_head), dim3(TREE_TQ * 4), 0, st, a);
   return hipGetLastError();
 }
 

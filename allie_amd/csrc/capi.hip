@@ -43,25 +43,43 @@ struct LayerW {
 
 constexpr int N_KINDS = 32;
 
-// Kernel probe: HIP events around every launch of one kernel kind inside the
-// forward, for the benchmark's roofline figure (process-wide, not re-entrant).
+// Kernel probe: for every op of one kind inside the forward, the op's main
+// kernel launch records a pair of HIP events at its own start and end, for
+// the benchmark's roofline figure (process-wide, not re-entrant).
 struct Probe {
   int kind = -1;
   int n = 0;
   std::vector<hipEvent_t> start, stop;
+  LaunchProbe armed;
+  bool is_armed = false, taken = false;
 } g_probe;
 
 hipError_t probe_mark(int kind, bool before, hipStream_t st) {
+  (void)st;
   if (g_probe.kind != kind) return hipSuccess;
   if (before) {
     if (g_probe.n >= (int)g_probe.start.size()) return hipSuccess;
-    return hipEventRecord(g_probe.start[g_probe.n], st);
+    g_probe.armed.start = g_probe.start[g_probe.n];
+    g_probe.armed.stop = g_probe.stop[g_probe.n];
+    g_probe.is_armed = true;
+    g_probe.taken = false;
+    return hipSuccess;
   }
-  if (g_probe.n >= (int)g_probe.stop.size()) return hipSuccess;
-  return hipEventRecord(g_probe.stop[g_probe.n++], st);
+  if (g_probe.taken) ++g_probe.n;  // an op without a probe-aware launch is not counted
+  g_probe.is_armed = g_probe.taken = false;
+  return hipSuccess;
 }
 
 }  // namespace
+
+namespace allie {
+LaunchProbe* launch_probe_take() {
+  if (!g_probe.is_armed) return nullptr;
+  g_probe.is_armed = false;
+  g_probe.taken = true;
+  return &g_probe.armed;
+}
+}  // namespace allie
 
 // Pinned host staging for the small host arrays of a call (lengths, group
 // starts): a copy from pageable memory would synchronise the stream, so the
@@ -418,7 +436,7 @@ int run_heads(const allie_model* m, const float* h, const void* h_add, const int
 
 // Workspace of an extend of n tokens in G groups.
 struct ExtendWS {
-  int32_t *group_start, *tiles, *self_slot, *status;
+  int32_t *group_start, *tiles, *self_slot, *status, *order;
   float* h;
   void *x, *qkv, *attn, *ff, *hx;
   float *z, *part;
@@ -438,6 +456,7 @@ ExtendWS layout_extend(const allie_model* m, int n, int G, char* base) {
   w.tiles = (int32_t*)take(((size_t)n / 64 + G + 1) * 4);  // >= sum of ceil(size / 64)
   w.self_slot = (int32_t*)take((size_t)n * 4);
   w.status = (int32_t*)take(4);
+  w.order = (int32_t*)take((size_t)n * 4);
   w.h = (float*)take((size_t)n * d * 4);
   w.x = take((size_t)n * d * a);
   w.qkv = take((size_t)n * 3 * d * a);
@@ -908,31 +927,41 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   xa.out = w.attn;
   xa.act_bf16 = act;
 
+  // one-token groups (decode steps) [0, n_dec) stream their keys with one
+  // wave per (token, head), the games with the most keys first (bf16)
+  const int n_dec = tree ? n1 : (xa.one_token_groups ? n_tok : 0);
+  if (act && n_dec > 0) HIP_TRY(launch_decode_order(xa, n_dec, w.order, st));
+  auto launch_decode = [&](int nd) -> hipError_t {
+    ExtendAttnArgs wa = xa;
+    wa.n = nd == n_groups ? n_tok : nd;
+    wa.one_token_groups = nd == n_groups ? xa.one_token_groups : 1;
+    wa.order = (act && wa.one_token_groups) ? w.order : nullptr;
+    return launch_attn_extend_wave(wa, st);
+  };
   const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff, w.part};
   const void* final_add = nullptr;
   rc = run_layers(m, acts, n_tok, w.self_slot, kv_pool, kv_pool_blocks,
                   [&](int layer) -> int {
                     xa.layer = layer;
-                    HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, true, st));
                     if (tree) {
                       if (n1 > 0) {
-                        ExtendAttnArgs wa = xa;
-                        wa.n = n1;
-                        wa.one_token_groups = 1;
                         HIP_TRY(probe_mark(ALLIE_PROBE_DECODE, true, st));
-                        HIP_TRY(launch_attn_extend_wave(wa, st));
+                        HIP_TRY(launch_decode(n1));
                         HIP_TRY(probe_mark(ALLIE_PROBE_DECODE, false, st));
                       }
+                      HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, true, st));
                       if (fan)
-                        HIP_TRY(launch_attn_extend_fan(xa, n1, st));
+                        HIP_TRY(launch_attn_extend_fan(xa, n1, n_groups, 0, st));
                       else
                         HIP_TRY(launch_attn_extend_tree(xa, st));
+                      HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, false, st));
                     } else {
+                      HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, true, st));
                       HIP_TRY(probe_mark(ALLIE_PROBE_DECODE, true, st));
-                      HIP_TRY(launch_attn_extend_wave(xa, st));
+                      HIP_TRY(launch_decode(n_groups));
                       HIP_TRY(probe_mark(ALLIE_PROBE_DECODE, false, st));
+                      HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, false, st));
                     }
-                    HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, false, st));
                     return ALLIE_OK;
                   },
                   st, &final_add);

@@ -1007,20 +1007,19 @@ hipError_t launch_mfma(const GemmArgs& a, hipStream_t st) {
       int grid = device_cus() & ~7;
       grid = grid < 8 ? 8 : grid;
       grid = tiles < grid ? tiles : grid;
-      hipLaunchKernelGGL(gemm_big_kernel<EPI>, dim3(grid), dim3(256), 0, st, a);
+      launch_timed(gemm_big_kernel<EPI>, dim3(grid), dim3(256), 0, st, a);
       return hipGetLastError();
     }
   }
   const int num_tm = (a.M + BM - 1) / BM, num_tn = a.N / BN;
   const int tiles = num_tm * num_tn;
   if (a.split > 1) {
-    hipLaunchKernelGGL((gemm_mfma_kernel<EPI, WT, OUT_PART>), dim3(tiles * a.split), dim3(NTHREADS), 0, st, a);
+    launch_timed(gemm_mfma_kernel<EPI, WT, OUT_PART>, dim3(tiles * a.split), dim3(NTHREADS), 0, st, a);
     const int64_t n4 = (int64_t)a.M * (a.N / 4);
     hipLaunchKernelGGL((splitk_reduce_kernel<EPI, WT == W_FP8, F32OUT>), dim3((unsigned)((n4 + 255) / 256)),
                        dim3(256), 0, st, a);
   } else {
-    hipLaunchKernelGGL((gemm_mfma_kernel<EPI, WT, F32OUT ? OUT_F32 : OUT_BF16>), dim3(tiles), dim3(NTHREADS), 0,
-                       st, a);
+    launch_timed(gemm_mfma_kernel<EPI, WT, F32OUT ? OUT_F32 : OUT_BF16>, dim3(tiles), dim3(NTHREADS), 0, st, a);
   }
   return hipGetLastError();
 }

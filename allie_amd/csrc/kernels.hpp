@@ -1,9 +1,27 @@
 // Launch interfaces of the Allie gfx950 kernels (host side of each .hip file).
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace allie {
+
+// ---------------------------------------------------------------- timing
+// The benchmark's per-kernel timing: while a probe is armed, the next
+// probe-aware launch (launch_timed) records the armed events at its own
+// start and end on the GPU (hipExtLaunchKernelGGL) and disarms it; other
+// launches are untouched.
+struct LaunchProbe {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+LaunchProbe* launch_probe_take();  // the armed probe (now disarmed), or null
+template <typename K, typename... Args>
+inline void launch_timed(K kernel, dim3 grid, dim3 block, uint32_t lds, hipStream_t st, Args... args) {
+  if (LaunchProbe* p = launch_probe_take())
+    hipExtLaunchKernelGGL(kernel, grid, block, lds, st, p->start, p->stop, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+}
 
 // ---------------------------------------------------------------- packing
 struct PackArgs {
@@ -162,9 +180,12 @@ struct ExtendAttnArgs {
   float scale;
   void* out;                   // [n][d]
   int act_bf16;
+  const int32_t* order;        // wave kernel: token of the i-th (token, head) row, or null (identity)
 };
 // one wave per (token, head), any group sizes, bf16 or fp32
 hipError_t launch_attn_extend_wave(const ExtendAttnArgs& a, hipStream_t st);
+// order[0 .. n) of the one-token groups 0 .. n - 1, most keys first
+hipError_t launch_decode_order(const ExtendAttnArgs& a, int n, int32_t* order, hipStream_t st);
 // MFMA tiles of TREE_TQ queries sharing a group's prefix, private keys as
 // columns (bf16); needs tiles
 constexpr int TREE_TQ = 128;
@@ -177,7 +198,8 @@ inline int fan_waves(int max_blocks) {
   const int ch = (max_blocks * KV_BLOCK + 63) / 64;
   return ch < 1 ? 1 : (ch > 8 ? 8 : ch);
 }
-hipError_t launch_attn_extend_fan(const ExtendAttnArgs& a, int g0, hipStream_t st);
+// groups [g0, g1); waves: 1..8, or 0 for fan_waves(max_blocks)
+hipError_t launch_attn_extend_fan(const ExtendAttnArgs& a, int g0, int g1, int waves, hipStream_t st);
 // tiles[] = (g << 8) | t for every tile_q-query tile t of every group g in
 // [first_group, n_groups), in order
 hipError_t launch_extend_tiles(const int32_t* group_start, int first_group, int n_groups, int tile_q, int32_t* tiles,

@@ -190,16 +190,18 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
                  int legal_words, const allie_outputs* out, void* kv_pool, int kv_pool_blocks,
                  int32_t* status, void* workspace, size_t workspace_bytes, void* stream);
 
-/* Kernel probe for benchmarks: while active, every launch of one kernel kind
- * inside allie_prefill is bracketed by HIP events on its stream;
- * allie_probe_end waits for them and returns the summed duration.  Not
- * re-entrant; the probed calls must all be on one device. */
+/* Kernel probe for benchmarks: while active, the main kernel of every op of
+ * one kind inside allie_prefill / allie_extend records HIP events at its own
+ * start and end on the GPU (hipExtLaunchKernelGGL); allie_probe_end waits for
+ * them and returns the summed duration and the count.  Not re-entrant; the
+ * probed calls must all be on one device.  No counterpart in the reference. */
 enum {
   ALLIE_PROBE_QKV = 0,  /* QKV projection GEMM */
-  ALLIE_PROBE_PROJ,     /* attention output projection GEMM (+ residual) */
+  ALLIE_PROBE_PROJ,     /* attention output projection GEMM */
   ALLIE_PROBE_FC,       /* MLP c_fc GEMM + gelu */
-  ALLIE_PROBE_FC2,      /* MLP c_proj GEMM (+ residual) */
-  ALLIE_PROBE_ATTN,     /* attention of a layer (prefill: varlen; extend: all its kernels) */
+  ALLIE_PROBE_FC2,      /* MLP c_proj GEMM */
+  ALLIE_PROBE_ATTN,     /* attention of a layer (prefill: varlen kernel; extend: the fan or tree kernel,
+                           else the decode kernel) */
   ALLIE_PROBE_DECODE    /* extend: the one-token-group (decode) attention kernel */
 };
 int allie_probe_begin(int kind, int max_launches);
