@@ -144,27 +144,30 @@ ALLIE_DEV u32x4_t fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
 // fp32 partial sums of one K split (reduced by splitk_reduce_kernel)
 enum { OUT_BF16 = 0, OUT_F32 = 1, OUT_PART = 2 };
 
-template <int EPI, int WT, int OUT>
+template <int EPI, int WT, int OUT, int BMT>
 __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
+  // block tile BMT (256 or 128) x BN; wave (wm, wn) owns WMX x 64
+  constexpr int FMT = BMT / 64, WMX = BMT / 2, ASTG = BMT * BK, AI = BMT / 64;
+  static_assert(4 * WMX * EP <= STAGES * (ASTG + W_STAGE), "epilogue region fits the ring");
   // one LDS arena: the ring of A stages, the ring of W stages; the epilogue
   // reuses it to transpose the output tile
-  __shared__ __attribute__((aligned(1024))) bf16_t smem[STAGES * (A_STAGE + W_STAGE)];
-  auto sA = [&](int s) { return smem + s * A_STAGE; };
-  auto sW = [&](int s) { return smem + STAGES * A_STAGE + s * W_STAGE; };
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[STAGES * (ASTG + W_STAGE)];
+  auto sA = [&](int s) { return smem + s * ASTG; };
+  auto sW = [&](int s) { return smem + STAGES * ASTG + s * W_STAGE; };
   constexpr bool FP8 = WT == W_FP8;
-  // vector-memory instructions per wave per k-tile: A 4, W 2 (bf16) or 1 (fp8)
-  constexpr int VMT = FP8 ? 5 : 6;
+  // vector-memory instructions per wave per k-tile: A BMT / 64, W 2 (bf16) or 1 (fp8)
+  constexpr int VMT = AI + (FP8 ? 1 : 2);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (LDS-DMA base)
   constexpr bool PART = OUT == OUT_PART;
-  const int num_tm = (a.M + BM - 1) / BM, num_tn = a.N / BN;
+  const int num_tm = (a.M + BMT - 1) / BMT, num_tn = a.N / BN;
   // K splits: block b computes split b / tiles of tile b % tiles
   const int n_tiles = PART ? gridDim.x / a.split : gridDim.x;
   const int split_id = PART ? blockIdx.x / n_tiles : 0;
   int tm, tn;
   tile_coords(PART ? blockIdx.x - split_id * n_tiles : blockIdx.x, n_tiles, num_tm, num_tn, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int m0 = tm * BMT, n0 = tn * BN;
   const int K = a.K;
   const int KT = K / BK / (PART ? a.split : 1);  // k-tiles of this block
   const int k_begin = split_id * KT * BK;
@@ -172,16 +175,16 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
   // ---- loader geometry ----------------------------------------------------
   // bf16 rows of 64 B, 16 rows per DMA instruction: lane -> row lane / 4,
   // physical chunk lane % 4, which holds logical chunk (lane % 4) ^ ((row >> 2) & 3).
-  // A: wave w fills rows [64 w, 64 w + 64) (4 instructions); W: rows
+  // A: wave w fills rows [BMT/4 w, BMT/4 (w + 1)) (AI instructions); W: rows
   // [32 w, 32 w + 32) (2 instructions).
   const int lr16 = lane >> 2;
   const int lc16 = (lane & 3) ^ ((lr16 >> 2) & 3);
   const bf16_t* __restrict__ A = reinterpret_cast<const bf16_t*>(a.A);
   // rows at or past M read the last valid row instead (results discarded)
-  const bf16_t* a_src[4];
+  const bf16_t* a_src[AI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    int m = m0 + wave * 64 + 16 * i + lr16;
+  for (int i = 0; i < AI; ++i) {
+    int m = m0 + wave * (BMT / 4) + 16 * i + lr16;
     m = m < a.M ? m : a.M - 1;
     a_src[i] = A + (int64_t)m * a.lda + lc16 * 8 + k_begin;
   }
@@ -198,7 +201,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
   auto issue = [&](int kt, int s) {
     const int k0 = kt * BK;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) g2l_16(a_src[i] + k0, sA(s) + (wave * 64 + 16 * i) * BK);
+    for (int i = 0; i < AI; ++i) g2l_16(a_src[i] + k0, sA(s) + (wave * (BMT / 4) + 16 * i) * BK);
     if constexpr (FP8) {
       g2l_16(w8_src + k0, reinterpret_cast<uint8_t*>(sW(s)) + wave * 32 * BK);
     } else {
@@ -212,11 +215,11 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
   const int n_base = n0 + wn * 64;
 
   // accumulator element (i, j, q, e) is output (m, n) with
-  // m = m0 + wm 128 + j 32 + frow, n = n_base + i 32 + q 8 + half 4 + e.
+  // m = m0 + wm WMX + j 32 + frow, n = n_base + i 32 + q 8 + half 4 + e.
   // bf16 weights: the accumulators start at the bias (fp8 weights scale the
   // sum first, so their bias is added in the epilogue; K splits add it in
   // the reduction).
-  f32x16_t acc[FN][FM];
+  f32x16_t acc[FN][FMT];
 #pragma unroll
   for (int i = 0; i < FN; ++i) {
     f32x16_t init{};
@@ -231,15 +234,15 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
       }
     }
 #pragma unroll
-    for (int j = 0; j < FM; ++j) acc[i][j] = init;
+    for (int j = 0; j < FMT; ++j) acc[i][j] = init;
   }
 
   // fragments of step `st` of the k-tile in stage s
-  auto load_a = [&](int s, int st, bf16x8_t(&xf)[FM]) {
+  auto load_a = [&](int s, int st, bf16x8_t(&xf)[FMT]) {
     const int c = 2 * half + st;
 #pragma unroll
-    for (int j = 0; j < FM; ++j) {
-      const int r = wm * 128 + j * 32 + frow;
+    for (int j = 0; j < FMT; ++j) {
+      const int r = wm * WMX + j * 32 + frow;
       xf[j] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(sA(s) + swz16(r, c)));
     }
   };
@@ -266,14 +269,14 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
       wf[i] = __builtin_bit_cast(bf16x8_t, st == 0 ? fp8x8_to_bf16x8(wq[i].x, wq[i].y)
                                                    : fp8x8_to_bf16x8(wq[i].z, wq[i].w));
   };
-  auto mfma_step = [&](const bf16x8_t(&wf)[FN], const bf16x8_t(&xf)[FM]) {
+  auto mfma_step = [&](const bf16x8_t(&wf)[FN], const bf16x8_t(&xf)[FMT]) {
 #pragma unroll
     for (int i = 0; i < FN; ++i)
 #pragma unroll
-      for (int j = 0; j < FM; ++j)
+      for (int j = 0; j < FMT; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], xf[j], acc[i][j], 0, 0, 0);
   };
-  constexpr int NMF = FN * FM;  // MFMAs per step
+  constexpr int NMF = FN * FMT;  // MFMAs per step
 
   // ---- prologue: fill the ring (tile 0 must land) ---------------------------
   const int n_pre = KT < STAGES ? KT : STAGES;
@@ -281,7 +284,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
   wait_vm_tiles<VMT>(n_pre - 1);
   lds_barrier();
 
-  bf16x8_t wP[FN], xP[FM], wQ[FN], xQ[FM];
+  bf16x8_t wP[FN], xP[FMT], wQ[FN], xQ[FMT];
   u32x4_t w8[FN];
   if constexpr (FP8) {
     load_w8(0, w8);
@@ -300,12 +303,12 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
       widen_w8(w8, 1, wQ);
       load_a(s, 1, xQ);
       mfma_step(wP, xP);
-      interleave_step<FM, NMF>();
+      interleave_step<FMT, NMF>();
     } else {
       load_w(s, 1, wQ);
       load_a(s, 1, xQ);
       mfma_step(wP, xP);
-      interleave_step<FN + FM, NMF>();
+      interleave_step<FN + FMT, NMF>();
     }
     // step 1: tile kt + 1 must have landed; then recycle stage s for tile
     // kt + STAGES and read the next tile's first fragments
@@ -321,13 +324,13 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
       load_w8(s1, w8);
       load_a(s1, 0, xP);
       mfma_step(wQ, xQ);
-      interleave_step<FN + FM, NMF>();
+      interleave_step<FN + FMT, NMF>();
       widen_w8(w8, 0, wP);
     } else {
       load_w(s1, 0, wP);
       load_a(s1, 0, xP);
       mfma_step(wQ, xQ);
-      interleave_step<FN + FM, NMF>();
+      interleave_step<FN + FMT, NMF>();
     }
   }
 
@@ -343,8 +346,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
       for (int q = 0; q < 4; ++q) {
         const int n = n_base + i * 32 + q * 8 + half * 4;
 #pragma unroll
-        for (int j = 0; j < FM; ++j) {
-          const int m = m0 + wm * 128 + j * 32 + frow;
+        for (int j = 0; j < FMT; ++j) {
+          const int m = m0 + wm * WMX + j * 32 + frow;
           if (m >= a.M) continue;
           *reinterpret_cast<float4*>(Cf + (int64_t)m * ldc + n) =
               make_float4(acc[i][j][q * 4 + 0], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
@@ -353,11 +356,11 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
     }
   } else {
     // bf16 results go through LDS so that global memory sees whole 128-byte
-    // row segments: each wave writes its 128 (m) x 64 (n) sub-tile into a
+    // row segments: each wave writes its WMX (m) x 64 (n) sub-tile into a
     // private region of rows padded to EP bf16, then reads it back 16 bytes
     // per lane, 8 lanes per row.
     lds_barrier();  // every wave is done with the ring
-    bf16_t* reg = smem + wave * 128 * EP;
+    bf16_t* reg = smem + wave * WMX * EP;
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
 #pragma unroll
@@ -369,7 +372,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
           scl = *reinterpret_cast<const float4*>(a.scale + n_base + nl);
         }
 #pragma unroll
-        for (int j = 0; j < FM; ++j) {
+        for (int j = 0; j < FMT; ++j) {
           const int ml = j * 32 + frow;
           float v0 = acc[i][j][q * 4 + 0], v1 = acc[i][j][q * 4 + 1];
           float v2 = acc[i][j][q * 4 + 2], v3 = acc[i][j][q * 4 + 3];
@@ -403,13 +406,13 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
       // interleaving them would expose the memory latency 16 times.
       float* __restrict__ Rp = a.R;
 #pragma unroll
-      for (int half8 = 0; half8 < 2; ++half8) {
+      for (int half8 = 0; half8 < WMX / 64; ++half8) {
         uint4 v[8];
         float4 h0[8], h1[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           const int ml = (half8 * 8 + u) * 8 + (lane >> 3);
-          const int m = m0 + wm * 128 + ml;
+          const int m = m0 + wm * WMX + ml;
           v[u] = *reinterpret_cast<const uint4*>(reg + ml * EP + cl);
           if (m < a.M) {
             const float4* r = reinterpret_cast<const float4*>(Rp + (int64_t)m * a.ldr + n_base + cl);
@@ -420,7 +423,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           const int ml = (half8 * 8 + u) * 8 + (lane >> 3);
-          const int m = m0 + wm * 128 + ml;
+          const int m = m0 + wm * WMX + ml;
           if (m >= a.M) continue;
           float4 x0 = h0[u], x1 = h1[u];
           x0.x += bf2f(v[u].x & 0xffffu); x0.y += bf2f(v[u].x >> 16);
@@ -434,9 +437,9 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
       }
     } else {
 #pragma unroll 4
-      for (int it = 0; it < 16; ++it) {
+      for (int it = 0; it < WMX / 8; ++it) {
         const int ml = it * 8 + (lane >> 3);
-        const int m = m0 + wm * 128 + ml;
+        const int m = m0 + wm * WMX + ml;
         const uint4 v = *reinterpret_cast<const uint4*>(reg + ml * EP + cl);
         if (m >= a.M) continue;
         *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(a.C) + (int64_t)m * a.ldc + n_base + cl) = v;
@@ -1011,15 +1014,20 @@ hipError_t launch_mfma(const GemmArgs& a, hipStream_t st) {
       return hipGetLastError();
     }
   }
-  const int num_tm = (a.M + BM - 1) / BM, num_tn = a.N / BN;
-  const int tiles = num_tm * num_tn;
+  const int bm = gemm_tile_m(a.M, a.N);
+  const int tiles = ((a.M + bm - 1) / bm) * (a.N / BN);
   if (a.split > 1) {
-    launch_timed(gemm_mfma_kernel<EPI, WT, OUT_PART>, dim3(tiles * a.split), dim3(NTHREADS), 0, st, a);
+    if (bm == 128)
+      launch_timed(gemm_mfma_kernel<EPI, WT, OUT_PART, 128>, dim3(tiles * a.split), dim3(NTHREADS), 0, st, a);
+    else
+      launch_timed(gemm_mfma_kernel<EPI, WT, OUT_PART, 256>, dim3(tiles * a.split), dim3(NTHREADS), 0, st, a);
     const int64_t n4 = (int64_t)a.M * (a.N / 4);
     hipLaunchKernelGGL((splitk_reduce_kernel<EPI, WT == W_FP8, F32OUT>), dim3((unsigned)((n4 + 255) / 256)),
                        dim3(256), 0, st, a);
+  } else if (bm == 128) {
+    launch_timed(gemm_mfma_kernel<EPI, WT, F32OUT ? OUT_F32 : OUT_BF16, 128>, dim3(tiles), dim3(NTHREADS), 0, st, a);
   } else {
-    launch_timed(gemm_mfma_kernel<EPI, WT, F32OUT ? OUT_F32 : OUT_BF16>, dim3(tiles), dim3(NTHREADS), 0, st, a);
+    launch_timed(gemm_mfma_kernel<EPI, WT, F32OUT ? OUT_F32 : OUT_BF16, 256>, dim3(tiles), dim3(NTHREADS), 0, st, a);
   }
   return hipGetLastError();
 }
@@ -1036,9 +1044,16 @@ bool gemm_mfma_supported(const GemmArgs& a) {
   return a.N % BN == 0 && a.K % BK == 0 && a.lda % 8 == 0 && a.M > 0;
 }
 
+int gemm_tile_m(int M, int N) {
+  // 256-row tiles unless that leaves fewer tiles than a 256-CU device has CUs
+  const int64_t tiles256 = (int64_t)((M + 255) / 256) * (N / BN);
+  return tiles256 < 256 ? 128 : 256;
+}
+
 int gemm_split_factor(int M, int N, int K) {
   if (M <= 0 || N % BN != 0 || K % BK != 0) return 1;
-  const int64_t tiles = (int64_t)((M + BM - 1) / BM) * (N / BN);
+  const int bm = gemm_tile_m(M, N);
+  const int64_t tiles = (int64_t)((M + bm - 1) / bm) * (N / BN);
   const int KT = K / BK;
   int s = 1;
   // double while the grid stays within one block per CU of a 256-CU device

@@ -115,6 +115,9 @@ bool gemm_mfma_supported(const GemmArgs& a);
 // and MLP projections with a store epilogue and adds them to the residual
 // stream in the following LayerNorm
 bool gemm_uses_persistent(const GemmArgs& a);
+// block rows of the 256x128-class kernel for an M x N output: 256, or 128
+// when 256-row tiles would not cover a 256-CU device
+int gemm_tile_m(int M, int N);
 // K splits the forward uses for an M x N x K MFMA GEMM: enough blocks for
 // every CU when the output tiles alone leave most idle (small M)
 int gemm_split_factor(int M, int N, int K);
