@@ -361,8 +361,8 @@ ALLIE_DEV uint32_t pk_f16(float a, float b) { return __builtin_bit_cast(uint32_t
 // Tree kernel: a tile of TQ = 16 NW queries of one group (NW waves of 16
 // queries on 16x16x32 MFMAs) and one head.  Keys arrive in chunks of 64,
 // staged in LDS (K bf16 rows swizzled by kswz; V fp16, 8-byte chunk j of row
-// r at j ^ (4 ((r >> 1) & 1)), read transposed), two chunks loading into registers
-// while one is multiplied.  First the
+// r at j ^ (4 ((r >> 1) & 1)), read transposed), DEPTH chunks loading into
+// registers while one is multiplied.  First the
 // group's prefix (query i sees positions below min(P, pos[i])), then the
 // tile's private keys as columns: for each extra index e, a run of
 // consecutive tokens whose e-th private key is the same pool slot (siblings'
@@ -373,7 +373,7 @@ constexpr int TREE_EB = 8;  // extra indices per column batch
 // K rows (bf16, 128 B): 16-byte chunk c of row r at c ^ kswz(r)
 ALLIE_DEV int kswz(int r) { return (r >> 1) & 7; }
 
-template <int NW>
+template <int NW, int DEPTH>
 __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttnArgs a) {
   constexpr int TQ = NW * 16, NT = NW * 64, PER = 512 / NT;  // PER: 16-byte K (and V) pieces per thread per chunk
   constexpr int NH = TQ / 64;                               // 64-token halves (column builder waves)
@@ -405,7 +405,10 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
   auto pblk = [&](int bi) { return bi < 64 ? s_blk[bi] : (bi < nbp ? valid_blk(btab[bi]) : -1); };
 
   // ---- loads: block table, queries, the private keys' slots --------------
-  if (tid < 64) s_blk[tid] = tid < nbp ? valid_blk(btab[tid]) : -1;
+  if (tid < 64) {  // the table row is read before the prefix length is known
+    const int v = tid < a.max_blocks ? btab[tid] : -1;
+    s_blk[tid] = tid < nbp ? valid_blk(v) : -1;
+  }
   const int qloc = wave * 16 + lq;  // tile-local query of this lane
   const bool q_ok = qloc < ntok;
   const int qi = q_first + (q_ok ? qloc : 0);
@@ -611,25 +614,35 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
   bool oA[PER], oB[PER];
   __syncthreads();  // s_blk is in
   if (nchp > 0) fetch(0, nchp, kA, vA, oA);  // the prefix's first chunks load while the columns are built
-  if (nchp > 1) fetch(1, nchp, kB, vB, oB);
+  if (DEPTH > 1 && nchp > 1) fetch(1, nchp, kB, vB, oB);
   for (int eb = 0; eb < a.max_extra || eb == 0; eb += TREE_EB) {
     const int ncols = build_columns(eb);
     const int ncp = eb == 0 ? nchp : 0;  // prefix chunks go with the first batch
     const int nch = ncp + (ncols + 63) / 64;
     if (ncp < 1 && nch > 0) fetch(0, ncp, kA, vA, oA);
-    if (ncp < 2 && nch > 1) fetch(1, ncp, kB, vB, oB);
-    for (int j = 0; j < nch; j += 2) {
-      __syncthreads();  // every wave is done with the previous chunk
-      stage(kA, vA, oA);
-      __syncthreads();
-      if (j + 2 < nch) fetch(j + 2, ncp, kA, vA, oA);
-      if (wave_busy) compute(j, ncp);
-      if (j + 1 >= nch) break;
-      __syncthreads();
-      stage(kB, vB, oB);
-      __syncthreads();
-      if (j + 3 < nch) fetch(j + 3, ncp, kB, vB, oB);
-      if (wave_busy) compute(j + 1, ncp);
+    if constexpr (DEPTH > 1) {
+      if (ncp < 2 && nch > 1) fetch(1, ncp, kB, vB, oB);
+      for (int j = 0; j < nch; j += 2) {
+        __syncthreads();  // every wave is done with the previous chunk
+        stage(kA, vA, oA);
+        __syncthreads();
+        if (j + 2 < nch) fetch(j + 2, ncp, kA, vA, oA);
+        if (wave_busy) compute(j, ncp);
+        if (j + 1 >= nch) break;
+        __syncthreads();
+        stage(kB, vB, oB);
+        __syncthreads();
+        if (j + 3 < nch) fetch(j + 3, ncp, kB, vB, oB);
+        if (wave_busy) compute(j + 1, ncp);
+      }
+    } else {
+      for (int j = 0; j < nch; ++j) {
+        __syncthreads();
+        stage(kA, vA, oA);
+        __syncthreads();
+        if (j + 1 < nch) fetch(j + 1, ncp, kA, vA, oA);
+        if (wave_busy) compute(j, ncp);
+      }
     }
   }
   if (!q_ok) return;  // no barriers below
@@ -762,8 +775,14 @@ __global__ __launch_bounds__(512, 4) void attn_extend_fan_kernel(ExtendAttnArgs 
     if (bi < a.max_blocks && bi * KV_BLOCK < P) v = btab[bi];
     return (v >= 0 && v < a.pool_blocks) ? v : -1;
   };
-  // lane j holds block j % 4 of the wave's chunk j / 4 (its first 16 chunks)
-  const int bt = table_entry(wave + W * (lane >> 2), lane & 3);
+  // lane j holds block j % 4 of the wave's chunk j / 4 (its first 16 chunks);
+  // the table row is read before the prefix length is known
+  int bt;
+  {
+    const int bi = (wave + W * (lane >> 2)) * 4 + (lane & 3);
+    const int v = bi < a.max_blocks ? btab[bi] : -1;
+    bt = (bi * KV_BLOCK < P && v >= 0 && v < a.pool_blocks) ? v : -1;
+  }
   // queries: B operand of S^T = K Q^T, query lq, dims 32 ks + 8 lg .. +7
   const bool q_ok = lq < nq;
   const int qi = i0 + (q_ok ? lq : 0);
@@ -990,8 +1009,12 @@ hipError_t launch_attn_extend_fan(const ExtendAttnArgs& a, int g0, int g1, int w
 hipError_t launch_attn_extend_tree(const ExtendAttnArgs& a, hipStream_t st) {
   if (!a.act_bf16 || a.tiles == nullptr) return hipErrorInvalidValue;
   if (a.n_tiles == 0) return hipSuccess;
-  if (a.tile_q != TREE_TQ) return hipErrorInvalidValue;
-  launch_timed(attn_extend_tree_kernel<TREE_TQ / 16>, dim3(a.n_tiles, a.n_head), dim3(TREE_TQ * 4), 0, st, a);
+  if (a.tile_q == 128)  // 8 waves, two chunks in flight
+    launch_timed(attn_extend_tree_kernel<8, 2>, dim3(a.n_tiles, a.n_head), dim3(512), 0, st, a);
+  else if (a.tile_q == 64)  // 4 waves, one chunk in flight (registers)
+    launch_timed(attn_extend_tree_kernel<4, 1>, dim3(a.n_tiles, a.n_head), dim3(256), 0, st, a);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

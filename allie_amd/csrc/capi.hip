@@ -848,7 +848,8 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
     if (n1 == g && sz == 1) n1 = g + 1;
     if (g >= n1) max_rest = sz > max_rest ? sz : max_rest;
   }
-  const int tile_q = TREE_TQ;  // queries per tree-kernel tile
+  // queries per tree-kernel tile: 128 when some group is larger than 64
+  const int tile_q = max_rest > 64 ? 128 : 64;
   int64_t n_tiles = 0;
   for (int g = n1; g < n_groups; ++g)
     n_tiles += (group_start_host[g + 1] - group_start_host[g] + tile_q - 1) / tile_q;

@@ -177,7 +177,7 @@ struct ExtendAttnArgs {
   const int32_t* n_extra;      // [n]
   int max_extra;
   const int32_t* tiles;        // tree kernel: (group << 8) | q_tile of tile_q queries
-  int n_tiles, tile_q;         // tile_q: TREE_TQ
+  int n_tiles, tile_q;         // tile_q: 64 or 128
   const void* pool;            // pool base (the kernel adds the layer offset)
   int pool_blocks, n_layer, layer;
   float scale;
@@ -189,9 +189,8 @@ struct ExtendAttnArgs {
 hipError_t launch_attn_extend_wave(const ExtendAttnArgs& a, hipStream_t st);
 // order[0 .. n) of the one-token groups 0 .. n - 1, most keys first
 hipError_t launch_decode_order(const ExtendAttnArgs& a, int n, int32_t* order, hipStream_t st);
-// MFMA tiles of TREE_TQ queries sharing a group's prefix, private keys as
+// MFMA tiles of tile_q queries sharing a group's prefix, private keys as
 // columns (bf16); needs tiles
-constexpr int TREE_TQ = 128;
 hipError_t launch_attn_extend_tree(const ExtendAttnArgs& a, hipStream_t st);
 // Groups g0 .. of at most FAN_MAX_Q tokens each (bf16): one workgroup of
 // fan_waves(max_blocks) waves per (group, head), the waves splitting the
