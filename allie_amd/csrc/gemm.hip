@@ -148,12 +148,13 @@ template <int EPI, int WT, int OUT, int BMT>
 __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
   // block tile BMT (256 or 128) x BN; wave (wm, wn) owns WMX x 64
   constexpr int FMT = BMT / 64, WMX = BMT / 2, ASTG = BMT * BK, AI = BMT / 64;
-  static_assert(4 * WMX * EP <= STAGES * (ASTG + W_STAGE), "epilogue region fits the ring");
+  constexpr int STG = BMT == 128 ? 4 : STAGES;  // ring stages (128-row tiles: one more in flight)
+  static_assert(4 * WMX * EP <= STG * (ASTG + W_STAGE), "epilogue region fits the ring");
   // one LDS arena: the ring of A stages, the ring of W stages; the epilogue
   // reuses it to transpose the output tile
-  __shared__ __attribute__((aligned(1024))) bf16_t smem[STAGES * (ASTG + W_STAGE)];
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[STG * (ASTG + W_STAGE)];
   auto sA = [&](int s) { return smem + s * ASTG; };
-  auto sW = [&](int s) { return smem + STAGES * ASTG + s * W_STAGE; };
+  auto sW = [&](int s) { return smem + STG * ASTG + s * W_STAGE; };
   constexpr bool FP8 = WT == W_FP8;
   // vector-memory instructions per wave per k-tile: A BMT / 64, W 2 (bf16) or 1 (fp8)
   constexpr int VMT = AI + (FP8 ? 1 : 2);
@@ -279,7 +280,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
   constexpr int NMF = FN * FMT;  // MFMAs per step
 
   // ---- prologue: fill the ring (tile 0 must land) ---------------------------
-  const int n_pre = KT < STAGES ? KT : STAGES;
+  const int n_pre = KT < STG ? KT : STG;
   for (int t = 0; t < n_pre; ++t) issue(t, t);
   wait_vm_tiles<VMT>(n_pre - 1);
   lds_barrier();
@@ -296,8 +297,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
   }
 
   for (int kt = 0; kt < KT; ++kt) {
-    const int s = kt % STAGES;
-    const int s1 = (kt + 1) % STAGES;
+    const int s = kt % STG;
+    const int s1 = (kt + 1) % STG;
     // step 0: read step 1's fragments, multiply step 0's
     if constexpr (FP8) {
       widen_w8(w8, 1, wQ);
@@ -311,14 +312,14 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
       interleave_step<FN + FMT, NMF>();
     }
     // step 1: tile kt + 1 must have landed; then recycle stage s for tile
-    // kt + STAGES and read the next tile's first fragments
+    // kt + STG and read the next tile's first fragments
     {
       int newer = KT - kt - 2;
-      newer = newer < STAGES - 2 ? newer : STAGES - 2;
+      newer = newer < STG - 2 ? newer : STG - 2;
       wait_vm_tiles<VMT>(newer > 0 ? newer : 0);
     }
     lds_barrier();
-    if (kt + STAGES < KT) issue(kt + STAGES, s);
+    if (kt + STG < KT) issue(kt + STG, s);
     // after the last tile these read a stale (in-bounds) stage, never used
     if constexpr (FP8) {
       load_w8(s1, w8);
