@@ -72,7 +72,7 @@ _SIGS = [
     ("allie_probe_end", C.c_int, [C.POINTER(C.c_float), C.POINTER(C.c_int)]),
     ("allie_gemm", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
-      C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p]),
+      C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     ("allie_gemm_splitk", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
       C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_size_t, C.c_void_p]),

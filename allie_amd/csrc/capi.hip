@@ -206,10 +206,15 @@ struct PrefillWS {
   int32_t *lens, *cu, *ids, *pos, *seq_of, *last, *blk_off, *tiles, *status, *slot, *order;
   int64_t* in_off;
   float* h;
-  void *x, *qkv, *attn, *ff, *hx;
+  void *x, *qkv, *attn, *ff, *hx, *wdq;
   float *z, *part;
   size_t total;
 };
+
+// bf16 copy of one layer's largest fp8 weight (4 d^2), fp8-weight models only
+size_t wdq_bytes(const allie_model* m) {
+  return m->cfg.mode == ALLIE_MODE_FP8W ? (size_t)4 * m->d * m->d * 2 : 0;
+}
 
 PrefillWS layout_prefill(const allie_model* m, int B, int T, char* base) {
   PrefillWS w{};
@@ -241,13 +246,15 @@ PrefillWS layout_prefill(const allie_model* m, int B, int T, char* base) {
   w.hx = take((size_t)B * d * a);
   w.z = (float*)take((size_t)B * m->NH * 4);
   w.part = (float*)take(part_bytes(m, T, B));
+  w.wdq = take(wdq_bytes(m));
   w.total = off;
   return w;
 }
 
 // part: workspace of the K-split partial sums (part_bytes), or null
+// wdq: [4 d^2] bf16 workspace for fp8 weights on the persistent kernel, or null
 int gemm(const allie_model* m, const void* A, const void* W, const float* bias, const float* scale,
-         void* C, float* R, int M, int N, int K, int epi, int probe_kind, float* part, hipStream_t st) {
+         void* C, float* R, int M, int N, int K, int epi, int probe_kind, float* part, void* wdq, hipStream_t st) {
   GemmArgs g{};
   g.A = A;
   g.W = W;
@@ -266,6 +273,7 @@ int gemm(const allie_model* m, const void* A, const void* W, const float* bias, 
   g.out_f32 = m->cfg.mode == ALLIE_MODE_FP32;
   g.split = (part && g.wtype != W_F32) ? gemm_split_factor(M, N, K) : 1;
   g.part = part;
+  g.wdq = g.wtype == W_FP8 ? wdq : nullptr;
   HIP_TRY(probe_mark(probe_kind, true, st));
   hipError_t e = launch_gemm(g, st);
   if (e != hipSuccess) return fail(ALLIE_ERR_HIP, "gemm M=%d N=%d K=%d: %s", M, N, K, hipGetErrorString(e));
@@ -281,12 +289,13 @@ struct Acts {
   void* attn; // [T][d]
   void* ff;   // [T][4d]
   float* part;  // K-split partial sums (part_bytes)
+  void* wdq;    // fp8 weights widened to bf16 for the persistent GEMM (wdq_bytes), or null
 };
 
 // Whether the M x N x K store GEMM of this model runs on the persistent
 // kernel (see gemm()): then the projection feeding the residual stream is
 // stored as bf16 and added in the LayerNorm that follows.
-bool store_is_persistent(const allie_model* m, int M, int N, int K, const float* part) {
+bool store_is_persistent(const allie_model* m, int M, int N, int K, const float* part, void* wdq) {
   GemmArgs g{};
   g.M = M;
   g.N = N;
@@ -297,6 +306,7 @@ bool store_is_persistent(const allie_model* m, int M, int N, int K, const float*
   g.wtype = m->cfg.mode == ALLIE_MODE_FP32 ? W_F32 : (m->cfg.mode == ALLIE_MODE_FP8W ? W_FP8 : W_BF16);
   g.out_f32 = m->cfg.mode == ALLIE_MODE_FP32;
   g.split = (part && g.wtype != W_F32) ? gemm_split_factor(M, N, K) : 1;
+  g.wdq = g.wtype == W_FP8 ? wdq : nullptr;
   return gemm_uses_persistent(g);
 }
 
@@ -322,13 +332,13 @@ int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slo
   ln.eps = m->cfg.eps;
   ln.y = w.x;
   ln.act_bf16 = act;
-  const bool fuse_proj = store_is_persistent(m, T, d, d, w.part);
-  const bool fuse_fc2 = store_is_persistent(m, T, d, 4 * d, w.part);
+  const bool fuse_proj = store_is_persistent(m, T, d, d, w.part, w.wdq);
+  const bool fuse_fc2 = store_is_persistent(m, T, d, 4 * d, w.part, w.wdq);
   *final_add = nullptr;
   int rc;
   for (int li = 0; li < L; ++li) {
     const LayerW& l = m->layers[li];
-    if ((rc = gemm(m, w.x, l.w_qkv, l.b_qkv, l.s_qkv, w.qkv, nullptr, T, 3 * d, d, EPI_STORE, ALLIE_PROBE_QKV, w.part, st))) return rc;
+    if ((rc = gemm(m, w.x, l.w_qkv, l.b_qkv, l.s_qkv, w.qkv, nullptr, T, 3 * d, d, EPI_STORE, ALLIE_PROBE_QKV, w.part, w.wdq, st))) return rc;
     if (kv_pool && kv_slot) {
       KVWriteArgs kw{};
       kw.qkv = w.qkv;
@@ -345,20 +355,20 @@ int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slo
     }
     if ((rc = attn(li))) return rc;
     if (fuse_proj) {
-      if ((rc = gemm(m, w.attn, l.w_o, l.b_o, l.s_o, w.x, nullptr, T, d, d, EPI_STORE, ALLIE_PROBE_PROJ, w.part, st))) return rc;
+      if ((rc = gemm(m, w.attn, l.w_o, l.b_o, l.s_o, w.x, nullptr, T, d, d, EPI_STORE, ALLIE_PROBE_PROJ, w.part, w.wdq, st))) return rc;
     } else {
-      if ((rc = gemm(m, w.attn, l.w_o, l.b_o, l.s_o, nullptr, w.h, T, d, d, EPI_RESID, ALLIE_PROBE_PROJ, w.part, st))) return rc;
+      if ((rc = gemm(m, w.attn, l.w_o, l.b_o, l.s_o, nullptr, w.h, T, d, d, EPI_RESID, ALLIE_PROBE_PROJ, w.part, w.wdq, st))) return rc;
     }
     ln.g = l.ln2_g;
     ln.b = l.ln2_b;
     ln.add = fuse_proj ? w.x : nullptr;
     ln.h_out = fuse_proj ? w.h : nullptr;
     HIP_TRY(launch_layernorm(ln, st));
-    if ((rc = gemm(m, w.x, l.w_fc, l.b_fc, l.s_fc, w.ff, nullptr, T, 4 * d, d, EPI_GELU, ALLIE_PROBE_FC, w.part, st))) return rc;
+    if ((rc = gemm(m, w.x, l.w_fc, l.b_fc, l.s_fc, w.ff, nullptr, T, 4 * d, d, EPI_GELU, ALLIE_PROBE_FC, w.part, w.wdq, st))) return rc;
     if (fuse_fc2) {
-      if ((rc = gemm(m, w.ff, l.w_pr, l.b_pr, l.s_pr, w.x, nullptr, T, d, 4 * d, EPI_STORE, ALLIE_PROBE_FC2, w.part, st))) return rc;
+      if ((rc = gemm(m, w.ff, l.w_pr, l.b_pr, l.s_pr, w.x, nullptr, T, d, 4 * d, EPI_STORE, ALLIE_PROBE_FC2, w.part, w.wdq, st))) return rc;
     } else {
-      if ((rc = gemm(m, w.ff, l.w_pr, l.b_pr, l.s_pr, nullptr, w.h, T, d, 4 * d, EPI_RESID, ALLIE_PROBE_FC2, w.part, st))) return rc;
+      if ((rc = gemm(m, w.ff, l.w_pr, l.b_pr, l.s_pr, nullptr, w.h, T, d, 4 * d, EPI_RESID, ALLIE_PROBE_FC2, w.part, w.wdq, st))) return rc;
     }
     if (li + 1 < L) {
       ln.g = m->layers[li + 1].ln1_g;
@@ -438,7 +448,7 @@ int run_heads(const allie_model* m, const float* h, const void* h_add, const int
 struct ExtendWS {
   int32_t *group_start, *tiles, *self_slot, *status, *order;
   float* h;
-  void *x, *qkv, *attn, *ff, *hx;
+  void *x, *qkv, *attn, *ff, *hx, *wdq;
   float *z, *part;
   size_t total;
 };
@@ -465,6 +475,7 @@ ExtendWS layout_extend(const allie_model* m, int n, int G, char* base) {
   w.hx = take((size_t)n * d * a);
   w.z = (float*)take((size_t)n * m->NH * 4);
   w.part = (float*)take(part_bytes(m, n, n));
+  w.wdq = take(wdq_bytes(m));
   w.total = off;
   return w;
 }
@@ -797,7 +808,7 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
   aa.out = w.attn;
   aa.act_bf16 = act;
 
-  const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff, w.part};
+  const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff, w.part, w.wdq};
   const void* final_add = nullptr;
   rc = run_layers(m, acts, (int)T, kv_pool ? w.slot : nullptr, kv_pool, kv_pool_blocks,
                   [&](int layer) -> int {
@@ -939,7 +950,7 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
     wa.order = (act && wa.one_token_groups) ? w.order : nullptr;
     return launch_attn_extend_wave(wa, st);
   };
-  const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff, w.part};
+  const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff, w.part, w.wdq};
   const void* final_add = nullptr;
   rc = run_layers(m, acts, n_tok, w.self_slot, kv_pool, kv_pool_blocks,
                   [&](int layer) -> int {
@@ -1005,7 +1016,7 @@ int allie_probe_end(float* total_ms_host, int* n_launches_host) {
 }
 
 int allie_gemm(const void* A, const void* W, const float* bias, const float* scale, void* C,
-               float* R, int M, int N, int K, int epi, int wtype, int out_f32, void* stream) {
+               float* R, int M, int N, int K, int epi, int wtype, int out_f32, void* wdq, void* stream) {
   if (!A || !W || M < 0 || N <= 0 || K <= 0) return fail(ALLIE_ERR_ARG, "bad gemm arguments");
   if (epi < EPI_STORE || epi > EPI_RESID || wtype < W_BF16 || wtype > W_FP8)
     return fail(ALLIE_ERR_ARG, "bad gemm mode");
@@ -1027,6 +1038,7 @@ int allie_gemm(const void* A, const void* W, const float* bias, const float* sca
   g.epi = epi;
   g.wtype = wtype;
   g.out_f32 = wtype == W_F32 ? 1 : out_f32;
+  g.wdq = wtype == W_FP8 ? wdq : nullptr;
   if (wtype != W_F32 && !gemm_mfma_supported(g))
     return fail(ALLIE_ERR_ARG, "MFMA gemm needs N %% 128 == 0 and K %% 32 == 0 (N=%d K=%d)", N, K);
   if (wtype == W_FP8 && out_f32) return fail(ALLIE_ERR_ARG, "fp8 gemm has bf16 output only");

@@ -496,8 +496,14 @@ constexpr int RING = STAGES * (A_STAGE + W_STAGE);  // 128 KiB
 constexpr int DMA = 8;              // DMA instructions per wave per k-tile and operand
 constexpr int EP = 72;              // epilogue chunk row pitch (bf16)
 constexpr int CHUNK = 32 * EP;      // one wave's epilogue region (bf16 elements)
-constexpr int BIAS = RING + 4 * CHUNK;  // 256 fp32 bias values of the tile
-constexpr int SMEM = BIAS + 4 * BN;     // bf16 elements: + a spare bias slot (149 KiB)
+// a tile's 256 fp32 bias values and 256 fp32 weight scales, in two slots by
+// tile parity (the next tile's land while this one's epilogue reads its
+// own), then a spare slot that absent ones are loaded into (bf16 elements)
+constexpr int BIAS = RING + 4 * CHUNK;
+constexpr int SCALE = BIAS + 2 * BN;
+constexpr int SLOT = 4 * BN;            // parity stride
+constexpr int SPARE = BIAS + 2 * SLOT;
+constexpr int SMEM = SPARE + 2 * BN;    // 152 KiB
 constexpr int STORES = 32;          // epilogue stores per wave per tile
 
 // element offset of logical 16-byte chunk c of row r in a stage
@@ -537,13 +543,26 @@ ALLIE_DEV int opaque_v(int v) {
   asm volatile("" : "+v"(v));
   return v;
 }
-// 16-byte LDS read the compiler's wait insertion does not track: the caller
-// waits (lgkmcnt) before using the result.  Used where the compiler would
+// LDS reads the compiler's wait insertion does not track, each statement
+// with its own wait (lgkmcnt(0)) so that no use or copy of a result can be
+// placed between a read and the wait.  Used where the compiler would
 // otherwise wait for every outstanding LDS DMA load.
-ALLIE_DEV float4 lds_read_f4(const void* p) {
-  float4 r;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p) : "memory");
-  return r;
+// 4 x 16 bytes at p, p + 32 B, p + 64 B, p + 96 B
+ALLIE_DEV void lds_read_f4x4_stride32(const void* p, float4 (&r)[4]) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:32\n\tds_read_b128 %2, %4 offset:64\n\t"
+      "ds_read_b128 %3, %4 offset:96\n\ts_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+      : "v"((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p)
+      : "memory");
+}
+// two 16-byte reads
+ALLIE_DEV void lds_read_f4x2(const void* p0, const void* p1, float4& r0, float4& r1) {
+  asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+               : "=&v"(r0), "=&v"(r1)
+               : "v"((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p0),
+                 "v"((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p1)
+               : "memory");
 }
 ALLIE_DEV uint32_t lds_off(const void* p) {
   return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
@@ -551,10 +570,14 @@ ALLIE_DEV uint32_t lds_off(const void* p) {
 ALLIE_DEV void lds_write_b64(void* p, uint2 v) {
   asm volatile("ds_write_b64 %0, %1" ::"v"(lds_off(p)), "v"(v) : "memory");
 }
-ALLIE_DEV u32x4_t lds_read_b128(const void* p) {
-  u32x4_t r;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(lds_off(p)) : "memory");
-  return r;
+// four 16-byte reads (untracked, with their wait, as lds_read_f4x2)
+ALLIE_DEV void lds_read_b128x4(const void* p0, const void* p1, const void* p2, const void* p3, u32x4_t (&r)[4]) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n\tds_read_b128 %1, %5\n\tds_read_b128 %2, %6\n\tds_read_b128 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+      : "v"(lds_off(p0)), "v"(lds_off(p1)), "v"(lds_off(p2)), "v"(lds_off(p3))
+      : "memory");
 }
 // An accumulator read where it is used (not all 256 copied out at once
 // after the k-loop)
@@ -564,7 +587,10 @@ ALLIE_DEV float acc_read(float v) {
   return r;
 }
 
-template <int EPI>
+// SCALED: weights that were fp8 (widened exactly to bf16 for this call) with
+// a per-output-channel scale: the accumulators start at 0 and the epilogue
+// takes acc * scale + bias (the 256x128 kernel's order for fp8 weights).
+template <int EPI, bool SCALED>
 __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
 #if defined(__HIP_DEVICE_COMPILE__)
   // the 256 x 256 geometry (shadows the 256 x 128 kernel's constants)
@@ -574,7 +600,8 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(1024))) bf16_t smem[big::SMEM];
   auto sA = [&](int s) { return smem + s * A_STAGE; };
   auto sW = [&](int s) { return smem + big::STAGES * A_STAGE + s * W_STAGE; };
-  const float* bias_lds = reinterpret_cast<const float*>(smem + big::BIAS);
+  auto bias_lds = [&](int par) { return reinterpret_cast<const float*>(smem + big::BIAS + par * big::SLOT); };
+  auto scale_lds = [&](int par) { return reinterpret_cast<const float*>(smem + big::SCALE + par * big::SLOT); };
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -632,10 +659,22 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
     return __builtin_amdgcn_make_buffer_rsrc(
         a.bias ? const_cast<float*>(a.bias + T.n0) : const_cast<void*>(a.A), (short)0, BN * 4, 0x00020000);
   };
-  // without a bias the slice lands in a spare region and the bias region
-  // holds zeros (the load count stays the same either way)
-  const int bias_dst = opaque_s(a.bias ? big::BIAS : big::BIAS + 2 * BN);
-  if (!a.bias) reinterpret_cast<float*>(smem + big::BIAS)[tid] = 0.f;
+  auto rsrc_S = [&](const Tile& T) {
+    return __builtin_amdgcn_make_buffer_rsrc(
+        (SCALED && a.scale) ? const_cast<float*>(a.scale + T.n0) : const_cast<void*>(a.A), (short)0, BN * 4,
+        0x00020000);
+  };
+  // without a bias the slice lands in the spare slot and the bias slots hold
+  // zeros (the load count stays the same either way); likewise the scale
+  // slice, which only SCALED reads
+  const int bias_dst = opaque_s(a.bias ? big::BIAS : big::SPARE);
+  const int scale_dst = opaque_s((SCALED && a.scale) ? big::SCALE : big::SPARE);
+  const int slot_step = opaque_s((a.bias ? big::SLOT : 0));
+  const int sslot_step = opaque_s(((SCALED && a.scale) ? big::SLOT : 0));
+  if (!a.bias) {
+    reinterpret_cast<float*>(smem + big::BIAS)[tid] = 0.f;
+    reinterpret_cast<float*>(smem + big::BIAS + big::SLOT)[tid] = 0.f;
+  }
   // DMA of k-tile kt's A rows (issue_a) or W rows (issue_w) into stage s
   auto issue_a = [&](const Tile& T, int kt, int s) {
     const uint32_t kb = (uint32_t)kt * BK * 2;
@@ -662,9 +701,13 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
     issue_a(T, kt, s);
     issue_w(T, kt, s);
   };
-  // a tile's head: its bias slice (wave w: 64 values) and its first two k-tiles
-  auto issue_head = [&](const Tile& T) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_B(T), (lds_void_t2*)(smem + bias_dst + wave * 128), 4,
+  // a tile's head: its bias and scale slices (wave w: 64 values each) into
+  // the slots of its parity, and its first two k-tiles
+  auto issue_head = [&](const Tile& T, int par) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_B(T), (lds_void_t2*)(smem + bias_dst + par * slot_step + wave * 128),
+                                             4, (uint32_t)(wave * 64 + lane) * 4, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_S(T),
+                                             (lds_void_t2*)(smem + scale_dst + par * sslot_step + wave * 128), 4,
                                              (uint32_t)(wave * 64 + lane) * 4, 0, 0, 0);
     issue(T, 0, 0);
     issue(T, 1, 1);
@@ -740,23 +783,28 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
   const int rl = lane >> 3, cl = (lane & 7) * 8;  // read-back: row rl + 8 it, columns cl .. cl + 7
   int t = blockIdx.x;
   Tile cur = make_tile(t);
-  issue_head(cur);
+  int par = 0;  // the current tile's bias / scale slot
+  issue_head(cur, par);
   bool first = true;
   while (true) {
-    // the tile's bias and k-tile 0 must land (k-tile 1 and the previous
-    // tile's stores may still be in flight)
+    // the tile's bias, scale and k-tile 0 must land (k-tile 1 and the
+    // previous tile's stores may still be in flight)
     if (first) big::wait_vm<2 * DMA>();
     else big::wait_vm<2 * DMA + big::STORES>();
     lds_barrier();
     const int n_wave = wn * 128;  // within the tile
-    // (the bias slice landed with k-tile 0; read untracked, see lds_read_f4)
-    const float* bl = bias_lds + n_wave + half * 4;
+    // (the bias slice landed with k-tile 0; read untracked, with its wait in
+    // the same statement)
+    const float* bl = bias_lds(par) + n_wave + half * 4;
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
       float4 b[4];
+      if constexpr (SCALED) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) b[q] = lds_read_f4(bl + i * 32 + q * 8);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        for (int q = 0; q < 4; ++q) b[q] = make_float4(0, 0, 0, 0);
+      } else {
+        lds_read_f4x4_stride32(bl + i * 32, b);
+      }
       f32x16_t init;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -786,7 +834,7 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
     Tile nxt;
     if (more) {
       nxt = make_tile(t_next);
-      issue_head(nxt);
+      issue_head(nxt, par ^ 1);
     }
 
     // ---- epilogue: 8 chunks of 32 rows x 64 columns through LDS -------------
@@ -804,6 +852,15 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
           for (int q = 0; q < 4; ++q) {
             float v0 = acc_read(acc[i][j][q * 4 + 0]), v1 = acc_read(acc[i][j][q * 4 + 1]);
             float v2 = acc_read(acc[i][j][q * 4 + 2]), v3 = acc_read(acc[i][j][q * 4 + 3]);
+            if constexpr (SCALED) {
+              const int col = n_wave + i * 32 + q * 8 + half * 4;
+              float4 sc, bi;
+              lds_read_f4x2(scale_lds(par) + col, bias_lds(par) + col, sc, bi);
+              v0 = fmaf(v0, sc.x, bi.x);
+              v1 = fmaf(v1, sc.y, bi.y);
+              v2 = fmaf(v2, sc.z, bi.z);
+              v3 = fmaf(v3, sc.w, bi.w);
+            }
             if constexpr (EPI == EPI_GELU) {
               round_bf16x2(v0, v1);
               round_bf16x2(v2, v3);
@@ -821,9 +878,8 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
         // (LDS operations of one wave run in order: the reads see the writes,
         // and the next chunk's writes come after these reads)
         u32x4_t v[4];
-#pragma unroll
-        for (int it = 0; it < 4; ++it) v[it] = lds_read_b128(reg + (it * 8 + rl) * EP + cl);
-        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3])::"memory");
+        lds_read_b128x4(reg + rl * EP + cl, reg + (8 + rl) * EP + cl, reg + (16 + rl) * EP + cl,
+                        reg + (24 + rl) * EP + cl, v);
 #pragma unroll
         for (int it = 0; it < 4; ++it) {
           // row wm 128 + j 32 + it 8 + rl, column n0 + n_wave + h 64 + cl
@@ -836,6 +892,7 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
     if (!more) break;
     t = t_next;
     cur = nxt;
+    par ^= 1;
     first = false;
   }
 #endif
@@ -979,7 +1036,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a) {
 // and a store or gelu epilogue whose 256 x 256 tiles fill every CU at least
 // once.
 bool use_big(const GemmArgs& a, int wt, bool f32out) {
-  if (wt != W_BF16 || f32out || a.split > 1 || a.epi == EPI_RESID) return false;
+  // fp8 weights take it when the call brings a bf16 buffer to widen them into
+  if ((wt != W_BF16 && !(wt == W_FP8 && a.wdq)) || f32out || a.split > 1 || a.epi == EPI_RESID) return false;
   if (a.N % big::BN != 0 || a.K % big::BK != 0 || a.K < 2 * big::BK) return false;
   // buffer offsets inside a tile are 32-bit
   if ((int64_t)big::BM * a.lda * 2 >= (int64_t)1 << 31 || (int64_t)big::BM * a.ldc * 2 >= (int64_t)1 << 31 ||
@@ -1002,6 +1060,23 @@ int device_cus() {
   return cus[dev];
 }
 
+// fp8 e4m3 weight bytes -> bf16 (exact; 3 mantissa bits fit in 7), 16 per thread
+__global__ __launch_bounds__(256) void widen_fp8_kernel(const uint4* __restrict__ w, uint4* __restrict__ out,
+                                                        int64_t n16) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n16) return;
+  const uint4 v = w[i];
+  const uint32_t b[4] = {v.x, v.y, v.z, v.w};
+  uint32_t o[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    o[2 * j] = fp8e4m3_to_bf16(b[j] & 0xffu) | (fp8e4m3_to_bf16((b[j] >> 8) & 0xffu) << 16);
+    o[2 * j + 1] = fp8e4m3_to_bf16((b[j] >> 16) & 0xffu) | (fp8e4m3_to_bf16(b[j] >> 24) << 16);
+  }
+  out[2 * i] = make_uint4(o[0], o[1], o[2], o[3]);
+  out[2 * i + 1] = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
 template <int EPI, int WT, bool F32OUT>
 hipError_t launch_mfma(const GemmArgs& a, hipStream_t st) {
   if constexpr (EPI != EPI_RESID) {
@@ -1011,7 +1086,26 @@ hipError_t launch_mfma(const GemmArgs& a, hipStream_t st) {
       int grid = device_cus() & ~7;
       grid = grid < 8 ? 8 : grid;
       grid = tiles < grid ? tiles : grid;
-      launch_timed(gemm_big_kernel<EPI>, dim3(grid), dim3(256), 0, st, a);
+      if constexpr (WT == W_FP8) {
+        // widen the fp8 weights to bf16 (exact) and scale in the epilogue
+        // (a probe times both launches: start with the widening, stop with
+        // the product)
+        const int64_t n16 = (int64_t)a.N * a.K / 16;
+        const dim3 wgrid((unsigned)((n16 + 255) / 256));
+        const uint4* w8 = reinterpret_cast<const uint4*>(a.W);
+        uint4* w16 = reinterpret_cast<uint4*>(a.wdq);
+        GemmArgs b = a;
+        b.W = a.wdq;
+        if (LaunchProbe* p = launch_probe_take()) {
+          hipExtLaunchKernelGGL(widen_fp8_kernel, wgrid, dim3(256), 0, st, p->start, nullptr, 0, w8, w16, n16);
+          hipExtLaunchKernelGGL((gemm_big_kernel<EPI, true>), dim3(grid), dim3(256), 0, st, nullptr, p->stop, 0, b);
+        } else {
+          hipLaunchKernelGGL(widen_fp8_kernel, wgrid, dim3(256), 0, st, w8, w16, n16);
+          hipLaunchKernelGGL((gemm_big_kernel<EPI, true>), dim3(grid), dim3(256), 0, st, b);
+        }
+      } else {
+        launch_timed(gemm_big_kernel<EPI, false>, dim3(grid), dim3(256), 0, st, a);
+      }
       return hipGetLastError();
     }
   }

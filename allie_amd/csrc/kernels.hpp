@@ -107,11 +107,13 @@ struct GemmArgs {
   int out_f32;         // store C as fp32 (else bf16)
   int split;           // K splits (MFMA kernels; <= 1: none)
   float* part;         // [split][M][N] fp32 partial sums when split > 1
+  void* wdq;           // W_FP8: [N][K] bf16 buffer the weights are widened into for the
+                       // persistent kernel (large M), or null
 };
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t st);
 bool gemm_mfma_supported(const GemmArgs& a);
 // true when this GEMM runs on the persistent 256 x 256 kernel (large M,
-// bf16 weights, store or gelu epilogue); the forward then writes attention
+// bf16 weights or fp8 with wdq, store or gelu epilogue); the forward then writes attention
 // and MLP projections with a store epilogue and adds them to the residual
 // stream in the following LayerNorm
 bool gemm_uses_persistent(const GemmArgs& a);

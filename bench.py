@@ -186,7 +186,8 @@ def run_prefill(args, cfg, mode, workload):
                       whole_forward_mfma_frac=flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS)
     res["roofline"] = {
         "kernel": ("gemm_big_kernel<EPI_GELU> (MLP c_fc, persistent 256x256 tiles)" if mode == "bfloat16"
-                   else "gemm_mfma_kernel<EPI_GELU,W_FP8> (MLP c_fc)"),
+                   else "widen_fp8_kernel + gemm_big_kernel<EPI_GELU,SCALED> (MLP c_fc, fp8 weights "
+                        "widened to bf16 per call, per-channel scale in the epilogue)"),
         "bound": "mfma", "achieved": fc_tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
         "frac": fc_tflops / MFMA_BF16_PEAK_TFLOPS,
         "traffic": read_traffic() if (mode == "bfloat16" and cfg.d_model == 1024) else None,

@@ -193,7 +193,9 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
 /* Kernel probe for benchmarks: while active, the main kernel of every op of
  * one kind inside allie_prefill / allie_extend records HIP events at its own
  * start and end on the GPU (hipExtLaunchKernelGGL); allie_probe_end waits for
- * them and returns the summed duration and the count.  Not re-entrant; the
+ * them and returns the summed duration and the count (a GEMM with fp8 weights
+ * on the persistent path: from the start of its widening kernel to the end of
+ * the product).  Not re-entrant; the
  * probed calls must all be on one device.  No counterpart in the reference. */
 enum {
   ALLIE_PROBE_QKV = 0,  /* QKV projection GEMM */
@@ -209,9 +211,11 @@ int allie_probe_end(float* total_ms_host, int* n_launches_host);
 
 /* Building blocks exported for tests and benchmarks.
  * GEMM: C[m][n] (+)= sum_k A[m][k] W[n][k] with the engine's epilogues
- * (0 store, 1 gelu, 2 residual add into R fp32); wtype 0 bf16, 1 fp32, 2 fp8. */
+ * (0 store, 1 gelu, 2 residual add into R fp32); wtype 0 bf16, 1 fp32, 2 fp8.
+ * wdq: fp8 only, optional device buffer of N * K bf16 that large-M GEMMs
+ * widen the weights into for the persistent kernel (the forward's path). */
 int allie_gemm(const void* A, const void* W, const float* bias, const float* scale, void* C,
-               float* R, int M, int N, int K, int epi, int wtype, int out_f32, void* stream);
+               float* R, int M, int N, int K, int epi, int wtype, int out_f32, void* wdq, void* stream);
 /* The same GEMM with K split into split_k parts (0: the split the forward
  * picks for this shape, allie_gemm_split_factor) whose fp32 partial sums go
  * to part (split * M * N floats), then one reduction pass applies the

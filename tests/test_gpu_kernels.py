@@ -116,7 +116,7 @@ def test_pack_status_flags():
     assert dev_pack(words, lens, pad_id=-1)["status"][0] == 0
 
 
-def _gemm(A, Wt, bias, epi, wtype, out_f32=False, R=None, scale=None):
+def _gemm(A, Wt, bias, epi, wtype, out_f32=False, R=None, scale=None, wdq=None):
     M, K = A.shape
     N = Wt.shape[0]
     dev = A.device
@@ -127,7 +127,7 @@ def _gemm(A, Wt, bias, epi, wtype, out_f32=False, R=None, scale=None):
     else:
         C_ = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
     rc = L.allie_gemm(capi.ptr(A), capi.ptr(Wt), capi.ptr(bias), capi.ptr(scale), capi.ptr(C_), capi.ptr(R),
-                      M, N, K, epi, wtype, int(out_f32), capi.stream_ptr())
+                      M, N, K, epi, wtype, int(out_f32), capi.ptr(wdq), capi.stream_ptr())
     capi.check(rc, "gemm")
     torch.cuda.synchronize()
     return C_
@@ -294,6 +294,32 @@ def test_gemm_fp8_weights(M, N, K, cuda):
     R = R0.clone()
     _gemm(A, qd, b, capi.EPI_RESID, capi.WT_FP8, R=R, scale=sd)
     assert ((R - (R0 + acc)).abs() <= acc.abs() * 2 ** -8 + 1e-4).all()
+
+
+@pytest.mark.parametrize("M,N,K", PERSISTENT_SHAPES)
+def test_gemm_fp8_weights_persistent(M, N, K, cuda):
+    """Large M with a widening buffer: the fp8 weights are widened to bf16
+    and the persistent kernel scales in the epilogue; same bars as the
+    256x128 kernel's fp8 path, store and gelu, bias on and off."""
+    g = torch.Generator(device="cpu").manual_seed(N + K + 1)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16).to(cuda)
+    w = torch.randn(N, K, generator=g) * 0.05
+    s = (w.abs().amax(1) / 448.0).float()
+    q = (w / s[:, None]).to(torch.float8_e4m3fn)
+    deq = q.float() * s[:, None]
+    qd, sd = q.view(torch.uint8).to(cuda), s.to(cuda)
+    wdq = torch.empty(N, K, dtype=torch.bfloat16, device=cuda)
+    for with_bias in (True, False):
+        b = rb(torch.randn(N, generator=g) * 0.1).to(cuda) if with_bias else None
+        acc = A.float() @ deq.to(cuda).T + (b if with_bias else 0)
+        C_ = _gemm(A, qd, b, capi.EPI_STORE, capi.WT_FP8, scale=sd, wdq=wdq).float()
+        assert ((C_ - acc).abs() <= acc.abs() * 2 ** -8 + 1e-4).all(), (with_bias, (C_ - acc).abs().max())
+        Cg = _gemm(A, qd, b, capi.EPI_GELU, capi.WT_FP8, scale=sd, wdq=wdq).float()
+        t = rb(acc)
+        ref = (0.5 * t) * (1 + torch.tanh(math.sqrt(2 / math.pi) * (t + 0.044715 * t ** 3)))
+        assert ((Cg - ref).abs() <= ref.abs() * 2 ** -6 + 2e-3).all(), (with_bias, (Cg - ref).abs().max())
+    # the widened weights are the exact fp8 values
+    assert torch.equal(wdq.float(), q.float().to(cuda))
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 256, 64), (300, 770, 256), (129, 2048, 1024)])

@@ -75,6 +75,24 @@ def test_prefill_tiny_perturbed(tiny, mode, tol, cuda):
     eng.close()
 
 
+@pytest.mark.parametrize("mode", ["bfloat16", "fp8w"])
+def test_prefill_tiny_large_batch(tiny, mode, cuda):
+    """256 games of 70..120 tokens (about 24k rows): the QKV and c_fc GEMMs
+    get at least 256 tiles of 256 x 256 and run on the persistent kernel (for
+    fp8 weights: widened to bf16 per call, scaled in the epilogue); 10 games
+    are checked against the oracle."""
+    cfg, sd = tiny
+    seqs, lens = synth_games(5, 256, 70, 120)
+    assert -(-int(lens.sum()) // 256) * 3 >= 256  # QKV: ceil(T / 256) m-tiles x 3 n-tiles
+    eng = Engine(cfg, sd, mode=mode)
+    got = run_engine(eng, seqs, lens)
+    pick = [0, 1, 2, 3, int(np.argmax(lens)), int(np.argmin(lens)), 100, 200, 254, 255]
+    ref = RefModel(cfg, sd, mode=mode).forward_last([(seqs[i] & 0x3FFF).astype(np.int64) for i in pick])
+    sub = {k: (v[pick] if v is not None else None) for k, v in got.items()}
+    check(sub, ref, 2e-2, f"{mode}-large-batch")
+    eng.close()
+
+
 def test_prefill_legal_mask_and_temperature(tiny, cuda):
     cfg, sd = tiny
     seqs, lens = synth_games(3, 9, 5, 60)
