@@ -24,6 +24,14 @@ Game rules (legal moves in python-chess order, game over) come from
 The reference's quirks are kept: MCTS evaluates the root twice (:407, :410),
 and the "rating-based" sampling rule reads the Elo of the side to move
 (:97-107).
+
+Beyond the reference, ``mcts`` and ``adaptive-mcts`` take ``kv_cache=True``:
+the search keeps its root's keys and values in a paged pool and evaluates
+each leaf as one new token over them (``allie_amd.search_kv``), with the same
+sequential semantics and results up to summation order; the root is then
+evaluated once.  ``leaf_batch=B`` (with ``kv_cache``) selects up to B leaves
+per round under virtual loss and evaluates them in one call, which is a
+different (batched) search.
 """
 from __future__ import annotations
 
@@ -34,6 +42,7 @@ from typing import Any, Optional
 import torch
 import torch.nn.functional as F
 
+from .search_kv import KVSearchCache, NodeEval, pool_nodes_for, virtual_loss_apply
 from .tokenizer import Game, UCITokenizer, apply_time_normalization, undo_time_normalization
 from .vocab import NUM_CHESS_MOVES, TIME_MEAN, TIME_STDEV
 
@@ -116,14 +125,23 @@ class Policy(DecodeStrategy):
         self.time_prediction = time_prediction
 
     def score_full(self, game: Game, legal_moves: list[str]) -> ScoreResult:
+        return self._score(game, legal_moves, self._full_eval(game))
+
+    def _full_eval(self, game: Game) -> NodeEval:
+        """The last token's outputs of the model call on the whole game."""
         outputs = self._forward(game)
-        logits = outputs["logits"][0, -1].float().cpu()
+        return NodeEval(outputs["logits"][0, -1].float().cpu(), float(outputs["value_logits"][0, -1].item()),
+                        float(outputs["time_logits"][0, -1].item()))
+
+    def _score(self, game: Game, legal_moves: list[str], ev: NodeEval) -> ScoreResult:
+        """decode.py:204-238 on one evaluation of the game."""
+        logits = ev.logits
         legal = torch.tensor([self.tokenizer.token_to_id[m] for m in legal_moves], dtype=torch.int64)
         move_logits = logits[legal]
-        time_encoding = float(outputs["time_logits"][0, -1].item())
+        time_encoding = ev.time
         think_time = undo_time_normalization(time_encoding) if self.time_prediction else None
         pov = 1 if game.white_to_move else -1
-        value = pov * float(outputs["value_logits"][0, -1].item())
+        value = pov * ev.value
         resigned_logit = logits[self.tokenizer.resigned_token_id].item()
         resigned = resigned_logit > move_logits.max().item() and value < -0.9
         all_probs = F.softmax(logits[:NUM_CHESS_MOVES] / self.temperature, dim=0)
@@ -135,7 +153,7 @@ class Policy(DecodeStrategy):
             all_probs,
             self.tokenizer.tokens[top_move_idx] in legal_moves,
             all_probs[legal].sum().item(),
-            float(outputs["value_logits"][0, -1].item()),
+            ev.value,
         )
 
 
@@ -190,7 +208,8 @@ def kl_regularised_policy(priors: torch.Tensor, values: torch.Tensor, visit_coun
 
 class MCTS(Policy):
     def init(self, n_sims: int = 50, depth_limit: int = 100, c_puct: float = 1.25, c_base: float = 19652.0,
-             dummy_value_function: bool = False, kl_reg_solution: bool = True, **kwargs) -> None:
+             dummy_value_function: bool = False, kl_reg_solution: bool = True, kv_cache: bool = False,
+             leaf_batch: int = 1, **kwargs) -> None:
         super().init(**kwargs)
         self.n_sims = n_sims
         self.depth_limit = depth_limit
@@ -199,9 +218,27 @@ class MCTS(Policy):
         self.dummy_value_function = dummy_value_function
         self.kl_reg_solution = kl_reg_solution
         self.total_rollouts = 0
+        self._init_kv(kv_cache, leaf_batch)
+
+    def _init_kv(self, kv_cache: bool, leaf_batch: int) -> None:
+        """Opt-in search over a paged KV cache (``allie_amd.search_kv``):
+        ``kv_cache=True`` evaluates each leaf as one new token over its
+        root's and ancestors' cached keys, with the reference's sequential
+        semantics; ``leaf_batch=B > 1`` also selects up to B leaves per round
+        under virtual loss and evaluates them in one call (a different,
+        batched search).  Neither exists in the reference."""
+        if leaf_batch < 1:
+            raise ValueError("leaf_batch must be >= 1")
+        if leaf_batch > 1 and not kv_cache:
+            raise ValueError("leaf_batch > 1 needs kv_cache=True")
+        self.kv_cache = kv_cache
+        self.leaf_batch = leaf_batch
+        self._kv: Optional[KVSearchCache] = None
 
     def check(self) -> None:
         assert callable(self.model), "model does not provide a value prediction"
+        if self.kv_cache:
+            assert hasattr(self.model, "engine"), "kv_cache needs the GPU model (allie_amd.model.AllieModel)"
 
     def _terminal_value(self, node: MCTSNode) -> Optional[float]:
         """decode.py:345-353: a draw is 0, a mate +1 for the side that moved."""
@@ -214,21 +251,28 @@ class MCTS(Policy):
         assert winner != node.game.white_to_move
         return 1.0
 
+    def _node_eval(self, node: MCTSNode) -> NodeEval:
+        kv = self._kv
+        if kv is not None and kv.can_extend(node):
+            return kv.evaluate([node])[0]
+        return self._full_eval(node.game)
+
     def _evaluate(self, node: MCTSNode):
         """One model evaluation of a node: (priors over its legal moves, value
         from the parent's point of view, normalised time)."""
-        outputs = self._forward(node.game)
+        ev = self._node_eval(node)
         legal = torch.tensor([self.tokenizer.token_to_id[m] for m in node.legal_moves], dtype=torch.int64)
-        logits = outputs["logits"][0, -1].float().cpu()[legal]
-        policy = F.softmax(logits, 0).tolist()
-        time_encoding = float(outputs["time_logits"][0, -1].item())
+        policy = F.softmax(ev.logits[legal], 0).tolist()
         pov = 1 if not node.game.white_to_move else -1  # black to move: the parent was white
-        value = pov * float(outputs["value_logits"][0, -1].item())
-        return policy, value, time_encoding
+        return policy, pov * ev.value, ev.time
 
     def _expand(self, node: MCTSNode, policy: list) -> None:
+        kv = self._kv if self._kv is not None and self._kv.active else None
         for action, prior in zip(node.legal_moves, policy):
-            node.children[action] = MCTSNode(prior, node.game.make_move(action))
+            child = MCTSNode(prior, node.game.make_move(action))
+            if kv is not None:
+                kv.attach(node, child, action)
+            node.children[action] = child
 
     def evaluate_node(self, node: MCTSNode) -> float:
         tv = self._terminal_value(node)
@@ -253,6 +297,8 @@ class MCTS(Policy):
             value = -value
 
     def _simulate(self, root: MCTSNode, n_sims: int) -> None:
+        if self.leaf_batch > 1 and self._kv is not None and self._kv.active:
+            return self._simulate_batched(root, n_sims)
         for _ in range(n_sims):
             node = root
             search_path = [node]
@@ -261,6 +307,47 @@ class MCTS(Policy):
                 search_path.append(node)
             value = self.evaluate_node(node)
             self.backup(search_path, value)
+
+    def _simulate_batched(self, root: MCTSNode, n_sims: int) -> None:
+        """Opt-in leaf batching: each round selects up to ``leaf_batch``
+        paths, the later ones under the virtual loss of the earlier ones,
+        evaluates the distinct leaves in one extend call, then backs every
+        path up with its leaf's value (a leaf picked twice is evaluated once
+        and backed up twice)."""
+        done = 0
+        while done < n_sims:
+            b = min(self.leaf_batch, n_sims - done)
+            paths = []
+            for _ in range(b):
+                node = root
+                path = [node]
+                while node.expanded() and len(path) <= self.depth_limit:
+                    node = self.select_child(node)
+                    path.append(node)
+                virtual_loss_apply(path, +1)
+                paths.append(path)
+            for path in paths:
+                virtual_loss_apply(path, -1)
+            leaves = list({id(p[-1]): p[-1] for p in paths}.values())
+            batch = [n for n in leaves if not n.expanded() and self._kv.can_extend(n)
+                     and self._terminal_value(n) is None]
+            if batch:
+                self._kv.evaluate(batch)  # memoised; evaluate_node below reads the results
+            values = {id(n): self.evaluate_node(n) for n in leaves}
+            for path in paths:
+                self.backup(path, values[id(path[-1])])
+            done += b
+
+    def _kv_begin(self, root: MCTSNode, game: Game, max_nodes: int) -> Optional[NodeEval]:
+        if not self.kv_cache:
+            return None
+        if self._kv is None:
+            self._kv = KVSearchCache(self.model.engine, self.tokenizer)
+        return self._kv.begin(root, game, max_nodes)
+
+    def _kv_end(self) -> None:
+        if self._kv is not None:
+            self._kv.end()
 
     def _final_policy(self, root: MCTSNode, legal_moves: list, policy_score: ScoreResult) -> ScoreResult:
         visit_counts = torch.FloatTensor([root.children[m].visit_count for m in legal_moves])
@@ -272,21 +359,30 @@ class MCTS(Policy):
                            policy_score.think_time, policy_score.resigned)
 
     def score_full(self, game: Game, legal_moves: list[str]) -> ScoreResult:
-        policy_score = super().score_full(game, legal_moves)
         root = MCTSNode(0.0, game)
-        self.evaluate_node(root)
-        self._simulate(root, self.n_sims)
+        ev = self._kv_begin(root, game, pool_nodes_for(self.n_sims, self.leaf_batch))
+        try:
+            # with the KV cache the root's one evaluation serves both calls
+            policy_score = self._score(game, legal_moves, ev) if ev is not None else super().score_full(game, legal_moves)
+            self.evaluate_node(root)
+            self._simulate(root, self.n_sims)
+        finally:
+            self._kv_end()
         self.total_rollouts += self.n_sims
         return self._final_policy(root, legal_moves, policy_score)
 
     def run_stats(self) -> dict:
-        return {"total_rollouts": self.total_rollouts}
+        st = {"total_rollouts": self.total_rollouts}
+        if self._kv is not None:
+            st["kv_leaf_evaluations"] = self._kv.n_evals
+        return st
 
 
 class AdaptiveMCTS(MCTS):
     def init(self, mean_n_sims: int = 50, depth_limit: int = 100, scale_c_puct: bool = True, c_puct: float = 1.25,
              c_base: float = 19652.0, dummy_value_function: bool = False, kl_reg_solution: bool = True,
-             use_human_move_time: bool = False, conversion_strategy: str = "linear", **kwargs) -> None:
+             use_human_move_time: bool = False, conversion_strategy: str = "linear", kv_cache: bool = False,
+             leaf_batch: int = 1, **kwargs) -> None:
         Policy.init(self, **kwargs)
         self.mean_n_sims = mean_n_sims
         self.depth_limit = depth_limit
@@ -300,6 +396,7 @@ class AdaptiveMCTS(MCTS):
         assert conversion_strategy in ["linear", "binary"]
         self.conversion_strategy = conversion_strategy
         self.total_rollouts = 0
+        self._init_kv(kv_cache, leaf_batch)
 
     def convert_time_to_sims(self, time_encoding: float) -> int:
         """decode.py:503-516."""
@@ -329,16 +426,20 @@ class AdaptiveMCTS(MCTS):
         return (0.0 if self.dummy_value_function else value), n_sims, think_time
 
     def score_full(self, game: Game, legal_moves: list[str]) -> ScoreResult:
-        policy_score = Policy.score_full(self, game, legal_moves)
         root = MCTSNode(0.0, game)
-        _, n_sims, _ = self.evaluate_root(root)
-        self.total_rollouts += n_sims
-        if n_sims == 0:
-            return ScoreResult(torch.FloatTensor([root.children[m].prior for m in legal_moves]),
-                               policy_score.think_time, policy_score.resigned)
-        if self.scale_c_puct:
-            self.c_puct = self.unscaled_c_puct * math.sqrt(self.mean_n_sims) / math.sqrt(n_sims)
-        self._simulate(root, n_sims)
+        ev = self._kv_begin(root, game, pool_nodes_for(200, self.leaf_batch))  # n_sims <= 200 (:516)
+        try:
+            policy_score = self._score(game, legal_moves, ev) if ev is not None else Policy.score_full(self, game, legal_moves)
+            _, n_sims, _ = self.evaluate_root(root)
+            self.total_rollouts += n_sims
+            if n_sims == 0:
+                return ScoreResult(torch.FloatTensor([root.children[m].prior for m in legal_moves]),
+                                   policy_score.think_time, policy_score.resigned)
+            if self.scale_c_puct:
+                self.c_puct = self.unscaled_c_puct * math.sqrt(self.mean_n_sims) / math.sqrt(n_sims)
+            self._simulate(root, n_sims)
+        finally:
+            self._kv_end()
         return self._final_policy(root, legal_moves, policy_score)
 
 

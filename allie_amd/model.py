@@ -42,6 +42,16 @@ class AllieModel:
         trainer.py:400-408)."""
         return cls(Engine(cfg, state_dict, mode=mode, device=device))
 
+    @classmethod
+    def from_checkpoint(cls, path: str, mode: str = BF16, device: str = "cuda:0",
+                        n_head: Optional[int] = None) -> "AllieModel":
+        """A reference ``best.pt`` (trainer.py:397-408), read as
+        evaluate.py:240-243 reads it; see ``allie_amd.checkpoint``."""
+        from .checkpoint import load_checkpoint
+
+        cfg, sd = load_checkpoint(path, n_head=n_head)
+        return cls.from_state_dict(cfg, sd, mode=mode, device=device)
+
     def eval(self) -> "AllieModel":
         return self
 

@@ -22,7 +22,9 @@ On the same JSON line:
 ``--config c3|c4|c5`` measures the other synthetic workloads, one JSON line
 each: MCTS tree expansion (leaf evals/s), continuous-batching self-play
 decode (tokens/s and step latency), and the fp8-weight 2x model (leaf
-evals/s, top-1 agreement with bf16).
+evals/s, top-1 agreement with bf16).  ``--config search`` times one MCTS
+decision (50 simulations) with the reference's per-leaf recompute, with the
+KV-cached search, and with KV plus leaf batching.
 """
 from __future__ import annotations
 
@@ -362,12 +364,72 @@ def bench_c4(args):
     return res
 
 
+# ------------------------------------------------------------------ search
+def search_games(n_games: int, plies: int, seed: int = 11):
+    """Seeded random legal games of ``plies`` moves (the search roots)."""
+    from allie_amd.tokenizer import Game
+
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n_games:
+        g = Game("300+0", 1500, 1600, None, False, [], [], None)
+        while len(g.moves) < plies and g.board.outcome() is None:
+            legal = g.legal_moves
+            g = g.make_move(legal[int(rng.integers(len(legal)))])
+        if len(g.moves) == plies and g.board.outcome() is None:
+            out.append(Game("300+0", 1500, 1600, None, False, g.moves, [3] * plies, None))
+    return out
+
+
+def bench_search(args):
+    """One MCTS decision (``score_full``, n_sims simulations) on the medium
+    bf16 model: the reference's full recompute per leaf, the KV-cached
+    search (same sequential semantics), and KV with leaf batching."""
+    import torch
+
+    from allie_amd import config, weights
+    from allie_amd.decode import DECODE_STRATEGIES
+    from allie_amd.model import AllieModel
+    from allie_amd.tokenizer import UCITokenizer
+
+    cfg = config.MEDIUM
+    n_sims = 50
+    model = AllieModel.from_state_dict(cfg, weights.init_weights(cfg, seed=0), mode="bfloat16")
+    tok = UCITokenizer(max_length=512)
+    games = search_games(args.warmup + args.steps, plies=60)
+    modes = {"recompute": {}, "kv": {"kv_cache": True}, "kv_batch16": {"kv_cache": True, "leaf_batch": 16}}
+    ms = {}
+    for name, kw in modes.items():
+        strat = DECODE_STRATEGIES["mcts"](model, tok, device="cuda", precision="bfloat16", n_sims=n_sims, **kw)
+        for g in games[: args.warmup]:
+            strat.score_full(g, g.legal_moves)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for g in games[args.warmup:]:
+            strat.score_full(g, g.legal_moves)
+        torch.cuda.synchronize()
+        ms[name] = (time.perf_counter() - t0) * 1000.0 / args.steps
+    model.close()
+    res = base_result(args, n_sims / (ms["kv"] / 1000.0), "simulations/s", ms["kv"], "bf16",
+                      "MCTS decision: medium 24x1024x16, 50 simulations, roots = random legal games of 60 plies "
+                      "(63 tokens)",
+                      ms_per_decision={k: round(v, 2) for k, v in ms.items()},
+                      sims_per_s={k: round(n_sims / (v / 1000.0), 1) for k, v in ms.items()},
+                      speedup_kv_vs_recompute=ms["recompute"] / ms["kv"],
+                      note="kv_batch16 is a different (virtual-loss batched) search; recompute and kv make "
+                           "the same decisions")
+    res["metric"] = "MCTS simulations/s per decision (not a SURVEY headline metric)"
+    res["roofline"] = None
+    res["cpu_baseline"] = None
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--config", choices=["c2", "c3", "c4", "c5"], default="c2")
+    ap.add_argument("--config", choices=["c2", "c3", "c4", "c5", "search"], default="c2")
     ap.add_argument("--slots", type=int, default=1024, help="c4: concurrent games")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
@@ -381,10 +443,10 @@ def main():
     if args.calibrate_copy:
         calibrate_copy()
         return
-    defaults = {"c2": (10, 3), "c3": (3, 1), "c4": (2000, 200), "c5": (10, 3)}[args.config]
+    defaults = {"c2": (10, 3), "c3": (3, 1), "c4": (2000, 200), "c5": (10, 3), "search": (5, 1)}[args.config]
     args.steps = defaults[0] if args.steps is None else args.steps
     args.warmup = defaults[1] if args.warmup is None else args.warmup
-    res = {"c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.config](args)
+    res = {"c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "search": bench_search}[args.config](args)
     print(json.dumps(res), flush=True)
 
 
