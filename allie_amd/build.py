@@ -1,7 +1,8 @@
 """Builds the gfx950 engine library ``allie_amd/liballie_amd.so`` in-tree.
 
 ``python -m allie_amd.build`` (or ``__graft_entry__.build()``) compiles every
-``csrc/*.hip`` with hipcc for gfx950 and links one shared library.  Each
+``csrc/*.hip`` with hipcc for gfx950 and links one shared library; the host
+rules library ``liballie_chess.so`` is built from ``csrc/*.cpp`` with g++.  Each
 translation unit compiles in parallel; the library is replaced atomically.
 """
 from __future__ import annotations
@@ -17,6 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "liballie_amd.so")
+CHESS_LIB = os.path.join(HERE, "liballie_chess.so")
 ARCH = os.environ.get("ALLIE_OFFLOAD_ARCH", "gfx950")
 
 # Packed fp32 instructions are kept out of every kernel (see DESIGN notes on
@@ -47,7 +49,26 @@ def _compile(src: str) -> str:
     return obj
 
 
+def build_chess(verbose: bool = False) -> str:
+    """The host rules library (``csrc/*.cpp``, no GPU code) with the host
+    C++ compiler."""
+    cxx = os.environ.get("CXX") or shutil.which("g++") or shutil.which("c++")
+    if not cxx:
+        raise RuntimeError("no host C++ compiler (g++) found")
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.cpp")))
+    tmp = CHESS_LIB + ".tmp"
+    cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", *srcs, "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"host build failed:\n{r.stderr}")
+    os.replace(tmp, CHESS_LIB)
+    if verbose:
+        print(f"built {CHESS_LIB}")
+    return CHESS_LIB
+
+
 def build(verbose: bool = False) -> str:
+    build_chess(verbose)
     os.makedirs(OBJ, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:

@@ -1039,8 +1039,10 @@ int allie_gemm(const void* A, const void* W, const float* bias, const float* sca
   g.wtype = wtype;
   g.out_f32 = wtype == W_F32 ? 1 : out_f32;
   g.wdq = wtype == W_FP8 ? wdq : nullptr;
-  if (wtype != W_F32 && !gemm_mfma_supported(g))
-    return fail(ALLIE_ERR_ARG, "MFMA gemm needs N %% 128 == 0 and K %% 32 == 0 (N=%d K=%d)", N, K);
+  if (wtype != W_F32 && !gemm_mfma_supported(g) && !gemm_skinny_supported(g))
+    return fail(ALLIE_ERR_ARG,
+                "gemm needs N %% 128 == 0 and K %% 32 == 0, or M <= %d, N %% 4 == 0 and K %% 8 == 0 (M=%d N=%d K=%d)",
+                SKINNY_MAX_M, M, N, K);
   if (wtype == W_FP8 && out_f32) return fail(ALLIE_ERR_ARG, "fp8 gemm has bf16 output only");
   if (wtype != W_F32 && out_f32 && epi != EPI_STORE)
     return fail(ALLIE_ERR_ARG, "fp32 output only with the store epilogue");

@@ -1159,6 +1159,7 @@ int gemm_split_factor(int M, int N, int K) {
 
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t st) {
   if (a.M == 0) return hipSuccess;
+  if (a.wtype != W_F32 && gemm_skinny_supported(a)) return launch_gemm_skinny(a, st);
   if (a.wtype == W_F32) {
     dim3 grid((a.N + 63) / 64, (a.M + 63) / 64);
     switch (a.epi) {

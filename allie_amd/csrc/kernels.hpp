@@ -112,6 +112,11 @@ struct GemmArgs {
 };
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t st);
 bool gemm_mfma_supported(const GemmArgs& a);
+// M <= SKINNY_MAX_M rows, bf16 or fp8 weights: one wave per 4 output columns
+// streams the weights once (launch_gemm picks it for such shapes)
+constexpr int SKINNY_MAX_M = 8;
+bool gemm_skinny_supported(const GemmArgs& a);
+hipError_t launch_gemm_skinny(const GemmArgs& a, hipStream_t st);
 // true when this GEMM runs on the persistent 256 x 256 kernel (large M,
 // bf16 weights or fp8 with wdq, store or gelu epilogue); the forward then writes attention
 // and MLP projections with a store epilogue and adds them to the residual

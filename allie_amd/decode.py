@@ -19,8 +19,9 @@ check mode or bf16), chosen when the model is built; ``precision`` is kept
 for signature compatibility (the reference wraps calls in torch autocast,
 decode.py:74-78).
 
-Game rules (legal moves in python-chess order, game over) come from
-``allie_amd.movegen`` because python-chess is absent from this image.
+Game rules (legal moves in python-chess order, game over) come from the
+native host rules (``allie_amd.rules``; ``allie_amd.movegen`` is their
+Python restatement) because python-chess is absent from this image.
 The reference's quirks are kept: MCTS evaluates the root twice (:407, :410),
 and the "rating-based" sampling rule reads the Elo of the side to move
 (:97-107).

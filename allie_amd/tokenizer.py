@@ -3,8 +3,8 @@
 Mirrors ``Game`` (src/modeling/data.py:40-80) and ``UCITokenizer``
 (data.py:175-337) of the reference, with one difference forced by the image:
 python-chess is absent, so ``Game.legal_moves`` is taken from the caller
-(``Game(..., legal=[...])``) or from ``allie_amd.movegen`` when that module
-can derive it.  The side to move is closed-form: white iff an even number of
+(``Game(..., legal=[...])``) or from the native host rules
+(``allie_amd.rules``, restated in Python by ``allie_amd.movegen``).  The side to move is closed-form: white iff an even number of
 moves has been played, because every game starts from the initial position
 (data.py:51-56).
 
@@ -53,16 +53,16 @@ class Game:
     @property
     def board(self):
         """The position after the game's moves (data.py:51-56), from the
-        host rules of ``allie_amd.movegen``; a child made by ``make_move``
-        extends its parent's cached board by one move."""
+        native host rules (``allie_amd.rules``); a child made by
+        ``make_move`` extends its parent's cached board by one move."""
         if self._board is None:
-            from . import movegen
+            from . import rules
 
             p = self._parent
             if p is not None and p._board is not None:
                 self._board = p._board.push_uci(self.moves[-1])
             else:
-                self._board = movegen.board_after(self.moves)
+                self._board = rules.board_after(self.moves)
             self._parent = None
         return self._board
 

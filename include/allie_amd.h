@@ -213,7 +213,9 @@ int allie_probe_end(float* total_ms_host, int* n_launches_host);
  * GEMM: C[m][n] (+)= sum_k A[m][k] W[n][k] with the engine's epilogues
  * (0 store, 1 gelu, 2 residual add into R fp32); wtype 0 bf16, 1 fp32, 2 fp8.
  * wdq: fp8 only, optional device buffer of N * K bf16 that large-M GEMMs
- * widen the weights into for the persistent kernel (the forward's path). */
+ * widen the weights into for the persistent kernel (the forward's path).
+ * Shapes (bf16 / fp8): N % 128 == 0 and K % 32 == 0, or M <= 8 rows with
+ * N % 4 == 0 and K % 8 == 0 (the skinny kernel, which such M always use). */
 int allie_gemm(const void* A, const void* W, const float* bias, const float* scale, void* C,
                float* R, int M, int N, int K, int epi, int wtype, int out_f32, void* wdq, void* stream);
 /* The same GEMM with K split into split_k parts (0: the split the forward

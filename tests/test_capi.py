@@ -1,6 +1,8 @@
-"""The C-ABI library loads on a CPU-only host and exports every function
-that include/*.h declares; the ctypes table binds exactly those names.
-No compute call is made (there is no GPU here)."""
+"""The C-ABI libraries load on a CPU-only host and export every function
+their headers declare (include/allie_amd.h: liballie_amd.so,
+include/allie_chess.h: liballie_chess.so); the ctypes tables bind exactly
+those names.  No compute call is made on the GPU library (there is no GPU
+here)."""
 import ctypes
 import glob
 import os
@@ -13,10 +15,10 @@ from allie_amd import capi
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def declared_signatures():
-    """name -> number of parameters, for every function in include/*.h."""
+def declared_signatures(header="allie_amd.h"):
+    """name -> number of parameters, for every function the header declares."""
     sigs = {}
-    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+    for h in [os.path.join(ROOT, "include", header)]:
         src = open(h).read()
         src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
         for m in re.finditer(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(allie_[a-z_0-9]+)\s*\(([^)]*)\)\s*;",
@@ -52,6 +54,26 @@ def test_library_exports_every_declared_symbol():
     assert L.allie_prefill_workspace_bytes(None, 1, 1) == 0
     assert L.allie_model_create(None, None) == -1
     assert b"NULL" in L.allie_last_error()
+
+
+def test_every_header_is_covered():
+    assert sorted(os.path.basename(h) for h in glob.glob(os.path.join(ROOT, "include", "*.h"))) == \
+        ["allie_amd.h", "allie_chess.h"]
+
+
+def test_chess_library_exports_every_declared_symbol():
+    from allie_amd import rules
+
+    if not os.path.exists(rules.LIB_PATH):
+        pytest.skip("library not built (run __graft_entry__.build())")
+    sigs = declared_signatures("allie_chess.h")
+    assert len(sigs) >= 8
+    lib = ctypes.CDLL(rules.LIB_PATH)
+    for name in sigs:
+        assert hasattr(lib, name), name
+    L = rules.lib()
+    for name, n_args in sigs.items():
+        assert len(getattr(L, name).argtypes) == n_args, name
 
 
 def test_library_missing_raises(monkeypatch, tmp_path):

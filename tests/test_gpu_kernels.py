@@ -322,6 +322,53 @@ def test_gemm_fp8_weights_persistent(M, N, K, cuda):
     assert torch.equal(wdq.float(), q.float().to(cuda))
 
 
+# skinny path (M <= 8 rows): the row counts of its three register variants
+# and their edges, one and four waves per workgroup (N < 2048), the medium
+# and 2x model's projection shapes, the heads' fp32 output (N = 2048), K not
+# a multiple of one step (512 or 2048 elements), and the first M past the
+# skinny range (the MFMA path)
+SKINNY_SHAPES = [(1, 3072, 1024), (2, 1024, 4096), (4, 4096, 1024), (5, 5120, 1280), (8, 2048, 1024),
+                 (7, 1024, 1024), (6, 1280, 5120), (3, 64, 8), (1, 1280, 1280), (9, 1024, 1024)]
+
+
+@pytest.mark.parametrize("M,N,K", SKINNY_SHAPES)
+def test_gemm_skinny_rows(M, N, K, cuda):
+    """M <= 8: the skinny kernel, every epilogue, bf16 and fp8 weights,
+    against the torch fp32 reference with the bars of the MFMA kernels;
+    repeated calls are bit-identical."""
+    g = torch.Generator(device="cpu").manual_seed(M * 13 + N + K)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16).to(cuda)
+    Wt = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16).to(cuda)
+    b = rb(torch.randn(N, generator=g) * 0.1).to(cuda)
+    acc = A.float() @ Wt.float().T + b
+    C_ = _gemm(A, Wt, b, capi.EPI_STORE, capi.WT_BF16).float()
+    assert ((C_ - acc).abs() <= acc.abs() * 2 ** -8 + 1e-5).all()
+    assert torch.equal(_gemm(A, Wt, b, capi.EPI_STORE, capi.WT_BF16).float(), C_)
+    C_nb = _gemm(A, Wt, None, capi.EPI_STORE, capi.WT_BF16).float()
+    acc_nb = acc - b
+    assert ((C_nb - acc_nb).abs() <= acc_nb.abs() * 2 ** -8 + 1e-5).all()
+    C32 = _gemm(A, Wt, b, capi.EPI_STORE, capi.WT_BF16, out_f32=True)
+    torch.testing.assert_close(C32, acc, rtol=1e-5, atol=1e-4)
+    Cg = _gemm(A, Wt, b, capi.EPI_GELU, capi.WT_BF16).float()
+    t = rb(acc)
+    ref = (0.5 * t) * (1 + torch.tanh(math.sqrt(2 / math.pi) * (t + 0.044715 * t ** 3)))
+    assert ((Cg - ref).abs() <= ref.abs() * 2 ** -6 + 2e-3).all()
+    R0 = torch.randn(M, N, generator=g).to(cuda)
+    R = R0.clone()
+    _gemm(A, Wt, b, capi.EPI_RESID, capi.WT_BF16, R=R)
+    assert ((R - (R0 + acc)).abs() <= acc.abs() * 2 ** -8 + 1e-5).all()
+    w = torch.randn(N, K, generator=g) * 0.05
+    s = (w.abs().amax(1) / 448.0).float()
+    q = (w / s[:, None]).to(torch.float8_e4m3fn)
+    accq = A.float() @ (q.float() * s[:, None]).to(cuda).T + b
+    qd, sd = q.view(torch.uint8).to(cuda), s.to(cuda)
+    Cq = _gemm(A, qd, b, capi.EPI_STORE, capi.WT_FP8, scale=sd).float()
+    assert ((Cq - accq).abs() <= accq.abs() * 2 ** -8 + 1e-4).all()
+    Rq = R0.clone()
+    _gemm(A, qd, b, capi.EPI_RESID, capi.WT_FP8, R=Rq, scale=sd)
+    assert ((Rq - (R0 + accq)).abs() <= accq.abs() * 2 ** -8 + 1e-4).all()
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 256, 64), (300, 770, 256), (129, 2048, 1024)])
 def test_gemm_fp32(M, N, K, cuda):
     g = torch.Generator(device="cpu").manual_seed(N * 3 + K)
