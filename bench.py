@@ -44,6 +44,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 HBM_PEAK_GBS = 8000.0
 METRIC = "leaf evals/sec @ medium, ragged batch 256; % of MFMA / HBM roofline"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gemm_fc_c2.txt")
+ATTN_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_attn_c3_c4.txt")
 
 
 def c2_batch():
@@ -63,15 +64,19 @@ def alg_flops(cfg, lens):
     return 2 * P * T + attn + heads
 
 
-def read_traffic():
-    """HBM bytes per launch of the fc GEMM, measured with rocprofv3 --pmc
-    FETCH_SIZE / WRITE_SIZE and scaled by the copy calibration (the line
-    ``hbm_bytes_per_launch: N`` of the committed summary), or None."""
-    if not os.path.exists(TRAFFIC_FILE):
+def read_traffic(key: str = ""):
+    """HBM bytes per launch of a dominant kernel, measured with rocprofv3
+    --pmc FETCH_SIZE / WRITE_SIZE and scaled by the copy calibration: the
+    line ``hbm_bytes_per_launch: N`` of the fc GEMM's committed summary, or
+    ``hbm_bytes_per_launch[key]: N`` of the attention kernels' one; None when
+    the summary is absent."""
+    path = TRAFFIC_FILE if not key else ATTN_TRAFFIC_FILE
+    tag = "hbm_bytes_per_launch:" if not key else f"hbm_bytes_per_launch[{key}]:"
+    if not os.path.exists(path):
         return None
-    with open(TRAFFIC_FILE) as f:
+    with open(path) as f:
         for line in f:
-            if line.startswith("hbm_bytes_per_launch:"):
+            if line.startswith(tag):
                 return float(line.split(":", 1)[1])
     return None
 
@@ -299,8 +304,8 @@ def bench_c3(args):
     res["roofline"] = {"kernel": "attn_extend_fan_kernel (level 1: 512 nodes in groups of 8 over 64 shared "
                                  "prefixes; level2: attn_extend_tree_kernel)",
                        "bound": "hbm", "achieved": a1["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                       "frac": a1["achieved_GBs"] / HBM_PEAK_GBS, "traffic": None,
-                       "level2": roof[2]}
+                       "frac": a1["achieved_GBs"] / HBM_PEAK_GBS, "traffic": read_traffic("c3_level1"),
+                       "level2": dict(roof[2], traffic=read_traffic("c3_level2"))}
     res["cpu_baseline"] = None
     eng.close()
     return res
@@ -357,7 +362,7 @@ def bench_c4(args):
                       moves_appended=appended, games_started=cb.games_started)
     res["roofline"] = {"kernel": "attn_extend_wave_kernel (decode: one token per running game over its paged KV)",
                        "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                       "frac": achieved / HBM_PEAK_GBS, "traffic": None, "avg_launch_ms": att_ms,
+                       "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic("c4_decode"), "avg_launch_ms": att_ms,
                        "alg_bytes_per_launch": att_bytes}
     res["cpu_baseline"] = None
     eng.close()
