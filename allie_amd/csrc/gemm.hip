@@ -1155,8 +1155,11 @@ int gemm_split_factor(int M, int N, int K) {
   const int KT = K / BK;
   int s = 1;
   // double while the grid stays within one block per CU of a 256-CU device
-  // and every split keeps at least 8 k-tiles
-  while (s < 8 && tiles * s * 2 <= 256 && KT % (s * 2) == 0 && KT / (s * 2) >= 8) s *= 2;
+  // and every split keeps at least 32 k-tiles (K >= 1024 per split): measured
+  // at M = 1024-2048, a K = 1024 projection is fastest unsplit (13 us against
+  // 18-20 us split 2-4 ways, the partial sums' traffic outweighing the extra
+  // blocks), and K = 4096 at 2-4 splits
+  while (s < 8 && tiles * s * 2 <= 256 && KT % (s * 2) == 0 && KT / (s * 2) >= 32) s *= 2;
   return s;
 }
 
