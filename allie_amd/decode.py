@@ -90,7 +90,11 @@ class DecodeStrategy:
 
     def decode_full(self, game: Game) -> DecodeResult:
         legal_moves = game.legal_moves
-        score = self.score_full(game, legal_moves)
+        return self._choose(game, legal_moves, self.score_full(game, legal_moves))
+
+    def _choose(self, game: Game, legal_moves: list[str], score: ScoreResult) -> DecodeResult:
+        """decode.py:97-113: argmax or a sample of the legal-move
+        probabilities, by ``sample`` (the "rating-based" rule included)."""
         probs = score.legal_move_probabilities
         if self.sample not in (True, False):
             assert self.sample == "rating-based"

@@ -24,7 +24,8 @@ each: MCTS tree expansion (leaf evals/s), continuous-batching self-play
 decode (tokens/s and step latency), and the fp8-weight 2x model (leaf
 evals/s, top-1 agreement with bf16).  ``--config search`` times one MCTS
 decision (50 simulations) with the reference's per-leaf recompute, with the
-KV-cached search, and with KV plus leaf batching.
+KV-cached search, and with KV plus leaf batching; ``--config serve``
+times 256 concurrent policy requests through the batching front end.
 """
 from __future__ import annotations
 
@@ -429,12 +430,75 @@ def bench_search(args):
     return res
 
 
+def bench_serve(args):
+    """256 concurrent ``policy`` requests (random legal games of 20-120
+    plies) on the medium bf16 model: the reference server's one-at-a-time
+    ``decode_full`` against the batching front end (allie_amd.serve)."""
+    import threading
+
+    import torch
+
+    from allie_amd import config, weights
+    from allie_amd.decode import DECODE_STRATEGIES
+    from allie_amd.model import AllieModel
+    from allie_amd.serve import PolicyBatcher
+    from allie_amd.tokenizer import UCITokenizer
+
+    cfg = config.MEDIUM
+    model = AllieModel.from_state_dict(cfg, weights.init_weights(cfg, seed=0), mode="bfloat16")
+    tok = UCITokenizer(max_length=512)
+    rng = np.random.default_rng(5)
+    n_req = 256
+    games = []
+    for p in rng.integers(20, 121, n_req):
+        games += search_games(1, int(p), seed=int(rng.integers(1 << 30)))
+    for g in games:
+        g.legal_moves  # host rules outside the timed region, as a server holds the position
+    seq = DECODE_STRATEGIES["policy"](model, tok, device="cuda", precision="bfloat16")
+    for g in games[:4]:
+        seq.decode_full(g)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for g in games[: 64]:
+        seq.decode_full(g)
+    torch.cuda.synchronize()
+    seq_rps = 64 / (time.perf_counter() - t0)
+    b = PolicyBatcher(DECODE_STRATEGIES["policy"](model, tok, device="cuda", precision="bfloat16"), max_batch=256,
+                      max_wait_ms=2.0)
+    futs = [None] * n_req
+    for rep in range(args.warmup + args.steps):
+        if rep == args.warmup:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+        ths = [threading.Thread(target=lambda i=i: futs.__setitem__(i, b.submit(games[i]))) for i in range(n_req)]
+        for t in ths:
+            t.start()
+        for t in ths:
+            t.join()
+        for f in futs:
+            f.result(timeout=300)
+    el = time.perf_counter() - t0
+    batches, reqs = b.batches, b.requests
+    b.close()
+    model.close()
+    rps = n_req * args.steps / el
+    res = base_result(args, rps, "requests/s", el * 1000 / args.steps, "bf16",
+                      "policy serving: medium 24x1024x16 bf16, 256 concurrent decode_full requests, random legal "
+                      "games of 20-120 plies",
+                      sequential_requests_per_s=seq_rps, speedup_vs_sequential=rps / seq_rps,
+                      mean_batch=reqs / max(batches, 1))
+    res["metric"] = "policy requests/s (not a SURVEY headline metric)"
+    res["roofline"] = None
+    res["cpu_baseline"] = None
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--config", choices=["c2", "c3", "c4", "c5", "search"], default="c2")
+    ap.add_argument("--config", choices=["c2", "c3", "c4", "c5", "search", "serve"], default="c2")
     ap.add_argument("--slots", type=int, default=1024, help="c4: concurrent games")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
@@ -448,10 +512,10 @@ def main():
     if args.calibrate_copy:
         calibrate_copy()
         return
-    defaults = {"c2": (10, 3), "c3": (3, 1), "c4": (2000, 200), "c5": (10, 3), "search": (5, 1)}[args.config]
+    defaults = {"c2": (10, 3), "c3": (3, 1), "c4": (2000, 200), "c5": (10, 3), "search": (5, 1), "serve": (5, 1)}[args.config]
     args.steps = defaults[0] if args.steps is None else args.steps
     args.warmup = defaults[1] if args.warmup is None else args.warmup
-    res = {"c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "search": bench_search}[args.config](args)
+    res = {"c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "search": bench_search, "serve": bench_serve}[args.config](args)
     print(json.dumps(res), flush=True)
 
 
