@@ -1154,12 +1154,16 @@ int gemm_split_factor(int M, int N, int K) {
   const int64_t tiles = (int64_t)((M + bm - 1) / bm) * (N / BN);
   const int KT = K / BK;
   int s = 1;
-  // double while the grid stays within one block per CU of a 256-CU device
-  // and every split keeps at least 32 k-tiles (K >= 1024 per split): measured
-  // at M = 1024-2048, a K = 1024 projection is fastest unsplit (13 us against
-  // 18-20 us split 2-4 ways, the partial sums' traffic outweighing the extra
-  // blocks), and K = 4096 at 2-4 splits
-  while (s < 8 && tiles * s * 2 <= 256 && KT % (s * 2) == 0 && KT / (s * 2) >= 32) s *= 2;
+  // double while every split keeps at least 8 k-tiles and the grid stays
+  // within a cap: 96 blocks for K < 2048, 256 for longer K.  Measured on the
+  // medium model's projections with weights cold in HBM (as in a forward):
+  // with few tiles (M <= 256) the extra blocks stream the weights faster
+  // (M = 63: K = 1024 at 4 splits 10-11 us against 11.5-15 us unsplit, and
+  // K = 4096 at 8 splits 13 us against 44 us); with ~100 tiles (M = 1500) a
+  // K = 1024 projection is fastest unsplit (13 us against 18 us at 2
+  // splits) while K = 4096 still gains at 2 (32 us against 46 us)
+  const int cap = K >= 2048 ? 256 : 96;
+  while (s < 8 && tiles * s * 2 <= cap && KT % (s * 2) == 0 && KT / (s * 2) >= 8) s *= 2;
   return s;
 }
 
