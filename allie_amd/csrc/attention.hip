@@ -5,7 +5,8 @@
 // causal mask, plus key padding at B > 1.  On a packed ragged stream the
 // padding disappears: query i of a game sees keys 0..i of the same game.
 //
-// attn_varlen_seq_kernel -- one workgroup of 8 waves per (game, 4 heads).
+// attn_varlen_seq_kernel -- one workgroup of 8 waves per (game, 4 heads), or per
+// (game, head) when there are fewer than 64 games.
 // A head's keys (bf16) and values (converted once to fp16, exact for bf16
 // values in fp16's range) of the whole game are staged in LDS (at most 512
 // tokens, 128 KiB); each wave then takes 32-query tiles in an order that
@@ -32,7 +33,9 @@ constexpr int HD = 64;           // head dim (GPT-2: d_model / n_head = 64)
 constexpr int MAX_KEYS_F32 = 512;  // fp32 kernel: keys per query held in LDS
 constexpr int SEQ_WAVES = 8;       // waves per workgroup of the per-game kernel
 constexpr int SEQ_MAXN = 512;      // longest game it stages (max_length)
-constexpr int SEQ_HEADS = 4;       // heads per workgroup (the next one loads during one)
+constexpr int SEQ_HEADS = 4;       // heads per workgroup (the next one loads during one), B >= SEQ_FEW
+constexpr int SEQ_FEW = 64;        // fewer games: one head per workgroup, so a batch of one
+                                   // game still spreads over n_head workgroups
 
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef __fp16 fp16x4_ll __attribute__((__vector_size__(4 * sizeof(__fp16))));
@@ -94,8 +97,9 @@ __global__ __launch_bounds__(SEQ_WAVES * 64, 1) void attn_varlen_seq_kernel(Attn
       *reinterpret_cast<uint4*>(sV + row * HD + ((ch ^ (((row >> 1) & 1) << 1)) << 3)) = h;
     }
   };
-  const int h_first = blockIdx.x * SEQ_HEADS;
-  const int h_end = h_first + SEQ_HEADS < a.n_head ? h_first + SEQ_HEADS : a.n_head;
+  const int hpw = (a.n_head + gridDim.x - 1) / gridDim.x;  // heads per workgroup (grid x = head groups)
+  const int h_first = blockIdx.x * hpw;
+  const int h_end = h_first + hpw < a.n_head ? h_first + hpw : a.n_head;
   load_head(h_first);
   store_head();
   __syncthreads();
@@ -330,8 +334,8 @@ hipError_t launch_attn_varlen(const AttnVarlenArgs& a, hipStream_t st) {
     if (a.B > 65535 || !a.order) return hipErrorInvalidValue;  // grid y limit; workspace
     if (!a.order_ready)
       hipLaunchKernelGGL(seq_order_kernel, dim3(1), dim3(ORDER_THREADS), 0, st, a.cu_seqlens, a.B, a.order);
-    launch_timed(attn_varlen_seq_kernel, dim3((a.n_head + SEQ_HEADS - 1) / SEQ_HEADS, a.B), dim3(SEQ_WAVES * 64), 0,
-                 st, a);
+    const int hpw = a.B < SEQ_FEW ? 1 : SEQ_HEADS;
+    launch_timed(attn_varlen_seq_kernel, dim3((a.n_head + hpw - 1) / hpw, a.B), dim3(SEQ_WAVES * 64), 0, st, a);
   } else {
     if (a.T == 0) return hipSuccess;
     hipLaunchKernelGGL(attn_varlen_f32_kernel, dim3((a.T + 3) / 4, a.n_head), dim3(256), 0, st, a);
