@@ -56,7 +56,7 @@ def build_chess(verbose: bool = False) -> str:
     if not cxx:
         raise RuntimeError("no host C++ compiler (g++) found")
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.cpp")))
-    tmp = CHESS_LIB + ".tmp"
+    tmp = f"{CHESS_LIB}.tmp{os.getpid()}"  # per process: concurrent first uses may build at once
     cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", *srcs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:

@@ -7,8 +7,8 @@ python-chess).  ``NativeBoard`` answers these in C++; it has the methods of
 ``allie_amd.movegen.Board`` that ``Game`` and the strategies use
 (``push_uci``, ``legal_uci``, ``outcome``, ``is_check``, ``is_game_over``),
 with the same results and move order.  The library is built by
-``allie_amd.build`` (``build()``); a missing library is an error, not a
-silent switch to another implementation.
+``allie_amd.build`` (``build()``), or on first use when it is missing; there
+is no switch to another implementation.
 """
 from __future__ import annotations
 
@@ -33,7 +33,11 @@ def lib():
         with _lock:
             if _lib is None:
                 if not os.path.exists(LIB_PATH):
-                    raise RuntimeError(f"{LIB_PATH} is missing: run python -m allie_amd.build")
+                    # host C++ only: built here on first use (g++, about two
+                    # seconds); a failed build raises
+                    from .build import build_chess
+
+                    build_chess()
                 L = C.CDLL(LIB_PATH)
                 vp = C.c_void_p
                 for name, res, args in (
