@@ -6,6 +6,9 @@ with ``chess.Board().push_uci``, ``Game.legal_moves`` lists
 ``board.is_game_over()`` / ``board.outcome()``, src/evaluation/decode.py:
 345-353).  python-chess is not installed in this image, so this module
 restates the rules of chess for games that start from the initial position.
+``Game`` uses the native library with the same rules and order
+(``allie_amd.rules``, csrc/chess.cpp); this Python restatement is what the
+tests compare it with, move list for move list.
 
 Move ORDER matters to the reference: ``decode_full`` breaks argmax ties by
 the order of ``legal_moves`` (decode.py:112) and MCTS expands children in
