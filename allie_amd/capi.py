@@ -68,6 +68,13 @@ _SIGS = [
       C.c_float, C.c_void_p, C.c_int, C.POINTER(AllieOutputs),  # temperature, legal, words, out
       C.c_void_p, C.c_int, C.c_void_p,                        # kv_pool, pool blocks, status
       C.c_void_p, C.c_size_t, C.c_void_p]),                   # workspace, bytes, stream
+    ("allie_extend_noalloc", C.c_int,
+     [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,            # model, ids, pos, n_tok
+      C.c_void_p, C.c_void_p, C.c_int,                        # group starts (host, device), n_groups
+      C.c_void_p, C.c_void_p, C.c_int,                        # prefix_len/blocks, max_blocks
+      C.c_void_p, C.c_void_p, C.c_int,                        # extra_slot, n_extra, max_extra
+      C.c_float, C.c_void_p, C.c_int, C.POINTER(AllieOutputs),  # temperature, legal, words, out
+      C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]),          # kv_pool, pool blocks, status, stream
     ("allie_probe_begin", C.c_int, [C.c_int, C.c_int]),
     ("allie_probe_end", C.c_int, [C.POINTER(C.c_float), C.POINTER(C.c_int)]),
     ("allie_gemm", C.c_int,

@@ -5,6 +5,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -70,6 +71,36 @@ hipError_t probe_mark(int kind, bool before, hipStream_t st) {
   return hipSuccess;
 }
 
+// Device scratch of allie_extend_noalloc: file-scope device memory, so that
+// entry point never allocates.  Every device the library runs on holds its
+// own copy until the process ends.  In host code `scratch` is only a handle
+// for hipGetSymbolAddress; the device address of each GPU's copy is looked up
+// once per device (scratch_init, from allie_model_create with that device
+// current) and only that address is passed to kernels.
+__device__ __align__(256) char scratch[ALLIE_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES] = {};
+
+// Records the current device's address of `scratch` (idempotent).
+hipError_t scratch_init(int dev) {
+  if (dev < 0 || dev >= MAX_DEVICES) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev]) return hipSuccess;
+  void* p = nullptr;
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return e;
+  g_scratch_ptr[dev] = p;
+  return hipSuccess;
+}
+
+void* scratch_ptr(int dev) {
+  if (dev < 0 || dev >= MAX_DEVICES) return nullptr;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  return g_scratch_ptr[dev];
+}
+
 }  // namespace
 
 namespace allie {
@@ -96,6 +127,7 @@ struct PinnedRing {
 
 struct allie_model {
   allie_config cfg;
+  int device = 0;          // the device current at allie_model_create (owns the arena)
   PinnedRing pinned;
   int d, H, hd, L, V, NH;  // NH: rows of the heads matrix (vocab + 2, padded)
   int wsz;                 // bytes per block-GEMM weight element
@@ -453,7 +485,8 @@ struct ExtendWS {
   size_t total;
 };
 
-ExtendWS layout_extend(const allie_model* m, int n, int G, char* base) {
+// with_wdq: include the fp8 widening buffer (only large-M GEMMs use it)
+ExtendWS layout_extend(const allie_model* m, int n, int G, char* base, bool with_wdq) {
   ExtendWS w{};
   size_t off = 0;
   auto take = [&](size_t bytes) -> char* {
@@ -475,7 +508,7 @@ ExtendWS layout_extend(const allie_model* m, int n, int G, char* base) {
   w.hx = take((size_t)n * d * a);
   w.z = (float*)take((size_t)n * m->NH * 4);
   w.part = (float*)take(part_bytes(m, n, n));
-  w.wdq = take(wdq_bytes(m));
+  w.wdq = with_wdq ? take(wdq_bytes(m)) : nullptr;
   w.total = off;
   return w;
 }
@@ -499,8 +532,16 @@ int allie_model_create(const allie_config* cfg, allie_model** out) {
   if (cfg->max_length <= 0 || cfg->max_length > 512 || cfg->max_length > cfg->n_positions)
     return fail(ALLIE_ERR_ARG, "max_length must be in [1, min(512, n_positions)]");
   if (cfg->mode < ALLIE_MODE_FP32 || cfg->mode > ALLIE_MODE_FP8W) return fail(ALLIE_ERR_ARG, "bad mode");
+  int dev = 0;
+  hipError_t de = hipGetDevice(&dev);
+  if (de != hipSuccess) return fail(ALLIE_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(de));
+  // address of this device's copy of the allocation-free scratch
+  de = scratch_init(dev);
+  if (de != hipSuccess)
+    return fail(ALLIE_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(de));
   allie_model* m = new allie_model();
   m->cfg = *cfg;
+  m->device = dev;
   m->d = cfg->d_model;
   m->H = cfg->n_head;
   m->hd = 64;
@@ -826,19 +867,32 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
 
 size_t allie_extend_workspace_bytes(const allie_model* m, int n_tok, int n_groups) {
   if (!m || n_tok < 0 || n_groups < 0) return 0;
-  return layout_extend(m, n_tok, n_groups, nullptr).total;
+  return layout_extend(m, n_tok, n_groups, nullptr, true).total;
 }
 
-int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_tok,
+}  // extern "C"
+
+namespace {
+
+// Checks an extend batch on the host; fills the plan of which attention
+// kernels run (see extend_run).
+struct ExtendPlan {
+  int n1 = 0;        // leading groups of one token each (decode steps)
+  int max_group = 0;
+  int max_rest = 0;  // largest group after those
+  int tile_q = 64;   // queries per tree-kernel tile
+  int64_t n_tiles = 0;
+};
+
+int extend_check(const allie_model* m, const int32_t* ids, const int32_t* pos, int n_tok,
                  const int32_t* group_start_host, int n_groups, const int32_t* prefix_len,
                  const int32_t* prefix_blocks, int max_blocks, const int32_t* extra_slot,
-                 const int32_t* n_extra, int max_extra, float temperature, const uint32_t* legal,
-                 int legal_words, const allie_outputs* out, void* kv_pool, int kv_pool_blocks,
-                 int32_t* status, void* workspace, size_t workspace_bytes, void* stream) {
+                 const int32_t* n_extra, int max_extra, const uint32_t* legal, int legal_words,
+                 const allie_outputs* out, void* kv_pool, int kv_pool_blocks, ExtendPlan* plan) {
   int rc = check_ready(m);
   if (rc) return rc;
   if (n_tok <= 0 || n_groups <= 0 || !ids || !pos || !group_start_host || !prefix_len ||
-      !extra_slot || !n_extra || !out || !kv_pool || !workspace || max_extra <= 0 || max_blocks < 0 ||
+      !extra_slot || !n_extra || !out || !kv_pool || max_extra <= 0 || max_blocks < 0 ||
       (max_blocks > 0 && !prefix_blocks) || kv_pool_blocks <= 0)
     return fail(ALLIE_ERR_ARG, "bad extend arguments");
   if (!out->value || !out->time || !out->top1 || !out->max_logit || !out->lse)
@@ -848,28 +902,35 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   if (group_start_host[0] != 0 || group_start_host[n_groups] != n_tok)
     return fail(ALLIE_ERR_ARG, "group_start must run from 0 to n_tok");
   if (n_groups > (1 << 23)) return fail(ALLIE_ERR_ARG, "too many groups");
-  int max_group = 0;
-  int n1 = 0;  // leading groups of one token each (decode steps)
-  int max_rest = 0;  // largest group after those
+  ExtendPlan p;
   for (int g = 0; g < n_groups; ++g) {
     const int sz = group_start_host[g + 1] - group_start_host[g];
     if (sz <= 0) return fail(ALLIE_ERR_ARG, "group %d is empty", g);
     if (sz > 64 * 256) return fail(ALLIE_ERR_ARG, "group %d has %d tokens (max 16384)", g, sz);
-    max_group = sz > max_group ? sz : max_group;
-    if (n1 == g && sz == 1) n1 = g + 1;
-    if (g >= n1) max_rest = sz > max_rest ? sz : max_rest;
+    p.max_group = sz > p.max_group ? sz : p.max_group;
+    if (p.n1 == g && sz == 1) p.n1 = g + 1;
+    if (g >= p.n1) p.max_rest = sz > p.max_rest ? sz : p.max_rest;
   }
   // queries per tree-kernel tile: 128 when some group is larger than 64
-  const int tile_q = max_rest > 64 ? 128 : 64;
-  int64_t n_tiles = 0;
-  for (int g = n1; g < n_groups; ++g)
-    n_tiles += (group_start_host[g + 1] - group_start_host[g] + tile_q - 1) / tile_q;
-  ExtendWS w = layout_extend(m, n_tok, n_groups, (char*)workspace);
-  if (workspace_bytes < w.total)
-    return fail(ALLIE_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, w.total);
-  hipStream_t st = (hipStream_t)stream;
+  p.tile_q = p.max_rest > 64 ? 128 : 64;
+  for (int g = p.n1; g < n_groups; ++g)
+    p.n_tiles += (group_start_host[g + 1] - group_start_host[g] + p.tile_q - 1) / p.tile_q;
+  *plan = p;
+  return ALLIE_OK;
+}
+
+// The extend forward over a laid-out workspace w whose w.group_start already
+// holds the group starts on the device (or group_start_dev, when given).
+int extend_run(allie_model* m, const ExtendPlan& plan, const ExtendWS& w, const int32_t* group_start_dev,
+               const int32_t* ids, const int32_t* pos, int n_tok, int n_groups, const int32_t* prefix_len,
+               const int32_t* prefix_blocks, int max_blocks, const int32_t* extra_slot, const int32_t* n_extra,
+               int max_extra, float temperature, const uint32_t* legal, int legal_words,
+               const allie_outputs* out, void* kv_pool, int kv_pool_blocks, int32_t* status, hipStream_t st) {
+  int rc;
   const int act = m->act_bf16;
-  if ((rc = upload_i32(m, w.group_start, group_start_host, (size_t)n_groups + 1, st))) return rc;
+  const int n1 = plan.n1, max_group = plan.max_group, max_rest = plan.max_rest, tile_q = plan.tile_q;
+  const int64_t n_tiles = plan.n_tiles;
+  const int32_t* group_start = group_start_dev ? group_start_dev : w.group_start;
   // the tree kernel shares a group's prefix across a tile of queries; groups of
   // one token (decode) stream it with one wave per query.  A batch that mixes
   // them (decode steps plus new games' prefixes) puts the one-token groups
@@ -878,8 +939,7 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   // groups of at most 16 tokens (MCTS children of one node) take the fan
   // kernel instead: the waves of a (group, head) split the prefix
   const bool fan = tree && max_rest <= FAN_MAX_Q;
-  if (tree && !fan) HIP_TRY(launch_extend_tiles(w.group_start, n1, n_groups, tile_q, w.tiles, st));
-
+  if (tree && !fan) HIP_TRY(launch_extend_tiles(group_start, n1, n_groups, tile_q, w.tiles, st));
   ExtendPrepArgs pa{};
   pa.n = n_tok;
   pa.n_groups = n_groups;
@@ -888,7 +948,7 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   pa.pool_blocks = kv_pool_blocks;
   pa.n_positions = m->cfg.n_positions;
   pa.pos = pos;
-  pa.group_start = w.group_start;
+  pa.group_start = group_start;
   pa.prefix_len = prefix_len;
   pa.prefix_blocks = prefix_blocks;
   pa.extra_slot = extra_slot;
@@ -921,7 +981,7 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   xa.n = n_tok;
   xa.one_token_groups = n1 == n_groups;
   xa.n_head = m->H;
-  xa.group_start = w.group_start;
+  xa.group_start = group_start;
   xa.n_groups = n_groups;
   xa.prefix_len = prefix_len;
   xa.prefix_blocks = prefix_blocks;
@@ -979,6 +1039,57 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
                   st, &final_add);
   if (rc) return rc;
   return run_heads(m, w.h, final_add, nullptr, n_tok, w.hx, w.z, temperature, legal, legal_words, out, w.part, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_tok,
+                 const int32_t* group_start_host, int n_groups, const int32_t* prefix_len,
+                 const int32_t* prefix_blocks, int max_blocks, const int32_t* extra_slot,
+                 const int32_t* n_extra, int max_extra, float temperature, const uint32_t* legal,
+                 int legal_words, const allie_outputs* out, void* kv_pool, int kv_pool_blocks,
+                 int32_t* status, void* workspace, size_t workspace_bytes, void* stream) {
+  ExtendPlan plan;
+  int rc = extend_check(m, ids, pos, n_tok, group_start_host, n_groups, prefix_len, prefix_blocks, max_blocks,
+                        extra_slot, n_extra, max_extra, legal, legal_words, out, kv_pool, kv_pool_blocks, &plan);
+  if (rc) return rc;
+  if (!workspace) return fail(ALLIE_ERR_ARG, "bad extend arguments");
+  ExtendWS w = layout_extend(m, n_tok, n_groups, (char*)workspace, true);
+  if (workspace_bytes < w.total)
+    return fail(ALLIE_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, w.total);
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = upload_i32(m, w.group_start, group_start_host, (size_t)n_groups + 1, st))) return rc;
+  return extend_run(m, plan, w, nullptr, ids, pos, n_tok, n_groups, prefix_len, prefix_blocks, max_blocks,
+                    extra_slot, n_extra, max_extra, temperature, legal, legal_words, out, kv_pool, kv_pool_blocks,
+                    status, st);
+}
+
+int allie_extend_noalloc(allie_model* m, const int32_t* ids, const int32_t* pos, int n_tok,
+                         const int32_t* group_start_host, const int32_t* group_start, int n_groups,
+                         const int32_t* prefix_len, const int32_t* prefix_blocks, int max_blocks,
+                         const int32_t* extra_slot, const int32_t* n_extra, int max_extra, float temperature,
+                         const uint32_t* legal, int legal_words, const allie_outputs* out, void* kv_pool,
+                         int kv_pool_blocks, int32_t* status, void* stream) {
+  ExtendPlan plan;
+  int rc = extend_check(m, ids, pos, n_tok, group_start_host, n_groups, prefix_len, prefix_blocks, max_blocks,
+                        extra_slot, n_extra, max_extra, legal, legal_words, out, kv_pool, kv_pool_blocks, &plan);
+  if (rc) return rc;
+  if (!group_start) return fail(ALLIE_ERR_ARG, "group_start (device copy) is required");
+  if (n_tok > ALLIE_NOALLOC_MAX_TOKENS)
+    return fail(ALLIE_ERR_WORKSPACE, "allie_extend_noalloc: %d tokens (max %d)", n_tok, ALLIE_NOALLOC_MAX_TOKENS);
+  // no fp8 widening buffer: at these row counts no GEMM runs on the persistent kernel
+  const size_t need = layout_extend(m, n_tok, n_groups, nullptr, false).total;
+  if (need > (size_t)ALLIE_NOALLOC_SCRATCH_BYTES)
+    return fail(ALLIE_ERR_WORKSPACE, "allie_extend_noalloc: %d tokens in %d groups need %zu bytes of scratch (max %zu)",
+                n_tok, n_groups, need, (size_t)ALLIE_NOALLOC_SCRATCH_BYTES);
+  char* base = (char*)scratch_ptr(m->device);
+  if (!base) return fail(ALLIE_ERR_STATE, "scratch of device %d not initialised", m->device);
+  ExtendWS w = layout_extend(m, n_tok, n_groups, base, false);
+  return extend_run(m, plan, w, group_start, ids, pos, n_tok, n_groups, prefix_len, prefix_blocks, max_blocks,
+                    extra_slot, n_extra, max_extra, temperature, legal, legal_words, out, kv_pool, kv_pool_blocks,
+                    status, (hipStream_t)stream);
 }
 
 int allie_probe_begin(int kind, int max_launches) {

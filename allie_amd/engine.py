@@ -198,14 +198,19 @@ class Engine:
     # --------------------------------------------------------------- extend
     def extend(self, ids, pos, group_sizes, prefix_len, prefix_blocks, extra_slot, n_extra,
                kv_pool: torch.Tensor, temperature: float = 1.0, legal=None, want_logits: bool = True,
-               status: Optional[torch.Tensor] = None, out: Optional[PrefillResult] = None) -> PrefillResult:
+               status: Optional[torch.Tensor] = None, out: Optional[PrefillResult] = None,
+               noalloc: bool = False) -> PrefillResult:
         """Forward of n new tokens over the paged KV cache (decode steps, MCTS
         tree levels).  Tokens come in groups of ``group_sizes`` (host ints);
         token i of group g attends the group's prefix (``prefix_len[g]``
         positions in blocks ``prefix_blocks[g]``) and then its own pool slots
         ``extra_slot[i, :n_extra[i]]``, the last of which receives its keys and
         values.  Array arguments are device int32 tensors (or numpy, copied).
-        Returns per-token outputs like ``prefill``."""
+        Returns per-token outputs like ``prefill``.
+
+        noalloc: run through ``allie_extend_noalloc`` (no workspace; the
+        library's per-device scratch, at most 256 tokens), which takes the
+        group starts as a device array."""
         dev = self.device
 
         def dt(a, shape=None):
@@ -234,11 +239,21 @@ class Engine:
         o = capi.AllieOutputs(capi.ptr(out.logits).value, capi.ptr(out.value).value, capi.ptr(out.time).value,
                               capi.ptr(out.top1).value, capi.ptr(out.max_logit).value, capi.ptr(out.lse).value)
         with torch.cuda.device(dev):
-            ws = self._workspace(int(self._lib.allie_extend_workspace_bytes(self._m, n, G)))
             legal_t = None
             if legal is not None:
                 legal_t = _as_tensor(legal).to(torch.int32).to(dev).contiguous()
                 assert legal_t.shape == (n, LEGAL_WORDS)
+            if noalloc:
+                gs_t = torch.from_numpy(group_start).to(dev)
+                rc = self._lib.allie_extend_noalloc(
+                    self._m, capi.ptr(ids_t), capi.ptr(pos_t), n, group_start.ctypes.data_as(C.c_void_p),
+                    capi.ptr(gs_t), G, capi.ptr(pl_t), capi.ptr(pb_t), pb_t.shape[1], capi.ptr(es_t), capi.ptr(ne_t),
+                    es_t.shape[1], float(temperature), capi.ptr(legal_t), LEGAL_WORDS if legal_t is not None else 0,
+                    C.byref(o), capi.ptr(kv_pool), self.pool_blocks(kv_pool), capi.ptr(status), capi.stream_ptr(),
+                )
+                capi.check(rc, "allie_extend_noalloc")
+                return out
+            ws = self._workspace(int(self._lib.allie_extend_workspace_bytes(self._m, n, G)))
             rc = self._lib.allie_extend(
                 self._m, capi.ptr(ids_t), capi.ptr(pos_t), n, group_start.ctypes.data_as(C.c_void_p), G,
                 capi.ptr(pl_t), capi.ptr(pb_t), pb_t.shape[1], capi.ptr(es_t), capi.ptr(ne_t), es_t.shape[1],

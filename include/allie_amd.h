@@ -190,6 +190,33 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
                  int legal_words, const allie_outputs* out, void* kv_pool, int kv_pool_blocks,
                  int32_t* status, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free extend.  No counterpart in the reference: an addition for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight search/serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results as allie_extend, except:
+ *   - no workspace: the call's scratch (activations, K-split partial sums,
+ *     tables) lives in a file-scope device array of
+ *     ALLIE_NOALLOC_SCRATCH_BYTES that each GPU holds until the process
+ *     ends (its per-device address is looked up in allie_model_create);
+ *   - group_start: the DEVICE copy of group_start_host (int32 [n_groups+1]),
+ *     so no host-to-device staging is needed; group_start_host is still read
+ *     on the host to plan the call;
+ *   - at most ALLIE_NOALLOC_MAX_TOKENS tokens, and the call's scratch layout
+ *     must fit the array (ALLIE_ERR_WORKSPACE otherwise; every shipped shape
+ *     -- small, medium, the 2x fp8 shape -- fits at the maximum).
+ * It calls no hipMalloc/hipFree/hipHostMalloc.  All calls on one GPU share
+ * that GPU's array, which keeps the last call's contents (nothing in it must
+ * start at zero): calls that overlap on one GPU (different streams or host
+ * threads without ordering) race and must not be issued. */
+#define ALLIE_NOALLOC_SCRATCH_BYTES (32u << 20)
+#define ALLIE_NOALLOC_MAX_TOKENS 256
+int allie_extend_noalloc(allie_model* m, const int32_t* ids, const int32_t* pos, int n_tok,
+                         const int32_t* group_start_host, const int32_t* group_start, int n_groups,
+                         const int32_t* prefix_len, const int32_t* prefix_blocks, int max_blocks,
+                         const int32_t* extra_slot, const int32_t* n_extra, int max_extra, float temperature,
+                         const uint32_t* legal, int legal_words, const allie_outputs* out, void* kv_pool,
+                         int kv_pool_blocks, int32_t* status, void* stream);
+
 /* Kernel probe for benchmarks: while active, the main kernel of every op of
  * one kind inside allie_prefill / allie_extend records HIP events at its own
  * start and end on the GPU (hipExtLaunchKernelGGL); allie_probe_end waits for
