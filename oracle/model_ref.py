@@ -22,11 +22,18 @@ Modes:
     evaluate.py:249; the fp32 check mode).
   * ``bfloat16`` -- emulation of torch CUDA autocast(bf16) (decode.py:74-78):
     GEMM operands and biases rounded to bf16, output of each GEMM rounded to
-    bf16 (``addmm``), LayerNorm/softmax/residual in fp32, ``gelu_new``
-    computed in fp32 from the bf16 GEMM output (``pow`` autocasts to fp32),
-    the Elo ``[e, 1-e] @ Wc`` matmul in bf16, heads rounded to bf16.
-    The exact torch 2.2 kernel choice is not pinnable here (parity of
-    rounding order is unpinned; tolerances absorb it).
+    bf16 (``addmm``), LayerNorm/residual in fp32, ``gelu_new`` computed in
+    fp32 from the bf16 GEMM output (CUDA autocast casts ``pow`` to fp32; CPU
+    autocast does not), the Elo ``[e, 1-e] @ Wc`` matmul in bf16, heads
+    rounded to bf16.  Attention follows torch's bf16
+    ``scaled_dot_product_attention`` kernels (autocast runs SDPA in bf16 on
+    the bf16 q/k/v): scores and softmax statistics in fp32, the
+    probabilities ``P = exp(s - rowmax)`` rounded to bf16 for the product
+    with V (fp32 accumulation), normalised by the fp32 row sum, output
+    rounded to bf16.  Pinned by tests/golden/model_tiny_bf16.npz (the
+    installed transformers GPT-2 under torch.autocast; tests/test_oracle_bf16.py).
+    Summation order is not pinnable: at 24 layers two orders differ by about
+    one bf16 ulp of the largest logits.
   * ``fp8w`` -- as ``bfloat16`` but the four block GEMMs use fp8 e4m3 weights
     with a per-output-channel fp32 scale applied to the fp32 accumulator (the
     weight itself is not rounded to bf16).
@@ -119,9 +126,14 @@ class RefModel:
         causal = torch.ones(T, T, dtype=torch.bool).tril()
         allowed = causal[None, None] & key_mask[:, None, None, :]
         s = s.masked_fill(~allowed, float("-inf"))
-        p = torch.softmax(s, dim=-1)
-        o = (p @ v).transpose(1, 2).reshape(B, T, d)
-        return o if self.mode == "float32" else rb(o)
+        if self.mode == "float32":
+            p = torch.softmax(s, dim=-1)
+            return (p @ v).transpose(1, 2).reshape(B, T, d)
+        # bf16 SDPA: P = exp(s - rowmax) enters the PV product as bf16; the
+        # row sum and the accumulation stay fp32
+        p = torch.exp(s - s.max(dim=-1, keepdim=True).values)
+        o = (rb(p) @ v) / p.sum(dim=-1, keepdim=True)
+        return rb(o.transpose(1, 2).reshape(B, T, d))
 
     def block(self, h: torch.Tensor, lw: dict, key_mask: torch.Tensor) -> torch.Tensor:
         eps = self.cfg.eps
