@@ -36,6 +36,7 @@ class AllieOutputs(C.Structure):
     _fields_ = [
         ("logits", C.c_void_p), ("value", C.c_void_p), ("time", C.c_void_p),
         ("top1", C.c_void_p), ("max_logit", C.c_void_p), ("lse", C.c_void_p),
+        ("logits_raw", C.c_void_p),
     ]
 
 
@@ -58,7 +59,7 @@ _SIGS = [
     ("allie_kv_block_bytes", C.c_size_t, [C.c_void_p]),
     ("allie_prefill", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_float, C.c_void_p, C.c_int,
-      C.POINTER(AllieOutputs), C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int,
+      C.POINTER(AllieOutputs), C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p,
       C.c_void_p, C.c_size_t, C.c_void_p]),
     ("allie_extend_workspace_bytes", C.c_size_t, [C.c_void_p, C.c_int, C.c_int]),
     ("allie_extend", C.c_int,

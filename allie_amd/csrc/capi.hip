@@ -466,6 +466,7 @@ int run_heads(const allie_model* m, const float* h, const void* h_add, const int
   ha.legal = legal;
   ha.legal_words = legal_words;
   ha.logits = out->logits;
+  ha.logits_raw = out->logits_raw;
   ha.value = out->value;
   ha.time = out->time;
   ha.top1 = out->top1;
@@ -760,7 +761,7 @@ size_t allie_kv_block_bytes(const allie_model* m) {
 int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_host, int n_seq,
                   float temperature, const uint32_t* legal, int legal_words,
                   const allie_outputs* out, void* kv_pool, int kv_pool_blocks, int first_block,
-                  const int32_t* kv_block_table, int kv_max_blocks,
+                  const int32_t* kv_block_table, int kv_max_blocks, int32_t* status,
                   void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_ready(m);
   if (rc) return rc;
@@ -814,7 +815,7 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
   p.block_table_in = kv_block_table;
   p.max_blocks_in = kv_max_blocks;
   p.pad_id = ALLIE_PAD_ID;
-  p.status = w.status;
+  p.status = status ? status : w.status;
   HIP_TRY(launch_pack(p, st));
 
   EmbedArgs ea{};

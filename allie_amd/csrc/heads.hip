@@ -8,10 +8,15 @@
 //   value  = tanh(z[value_col])         (value head Linear + Tanh)
 //   time   = z[time_col]                (time head Linear)
 // rounded to bf16 at the points torch autocast rounds them when
-// emulate_bf16 is set; and, over the move logits 0..n_moves-1 divided by the
+// emulate_bf16 is set (logits_raw, when given, receives z before that
+// rounding); and, over the move logits 0..n_moves-1 divided by the
 // temperature (optionally restricted to a legal-move bitmask):
 //   top1 = first index of the maximum (torch.argmax picks the first),
 //   max_logit, lse = logsumexp.
+// The reference takes the argmax of softmax(logits / T) (decode.py:223-226,
+// 112): a NaN or +inf among the considered logits makes that whole softmax
+// NaN and torch.argmax then returns its first element, so such a row gets
+// top1 = the first considered move id, and max_logit = lse = NaN.
 // One workgroup per game.
 #include "common.hpp"
 #include "kernels.hpp"
@@ -27,8 +32,11 @@ __global__ __launch_bounds__(256) void heads_kernel(HeadsArgs a) {
   const float* z = a.z + (int64_t)b * a.ldz;
   float best = -INFINITY;
   int best_i = 0x7fffffff;
+  int first_ok = 0x7fffffff;  // first considered move id
+  bool nonfinite = false;     // a considered logit / T is NaN or +inf
   for (int c = tid; c < a.vocab; c += 256) {
     float l = z[c];
+    if (a.logits_raw) a.logits_raw[(int64_t)b * a.vocab + c] = l;
     if (a.emulate_bf16) l = round_bf16(l);
     if (a.logits) a.logits[(int64_t)b * a.vocab + c] = l;
     if (c < a.n_moves) {
@@ -36,6 +44,8 @@ __global__ __launch_bounds__(256) void heads_kernel(HeadsArgs a) {
       if (a.legal) ok = (a.legal[(int64_t)b * a.legal_words + (c >> 5)] >> (c & 31)) & 1u;
       if (ok) {
         const float x = l / temperature;
+        first_ok = c < first_ok ? c : first_ok;
+        if (!(x < INFINITY)) nonfinite = true;  // NaN or +inf
         if (x > best) {  // c increases per thread: keeps the first maximum
           best = x;
           best_i = c;
@@ -46,6 +56,13 @@ __global__ __launch_bounds__(256) void heads_kernel(HeadsArgs a) {
   __shared__ float sv[4];
   __shared__ int si[4];
   __shared__ float ssum[4];
+  __shared__ int sfirst[4];
+  nonfinite = __syncthreads_or(nonfinite);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const int of = __shfl_xor(first_ok, o, 64);
+    first_ok = of < first_ok ? of : first_ok;
+  }
   // wave argmax, ties to the lower index
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
@@ -60,6 +77,7 @@ __global__ __launch_bounds__(256) void heads_kernel(HeadsArgs a) {
   if (lane == 0) {
     sv[w] = best;
     si[w] = best_i;
+    sfirst[w] = first_ok;
   }
   __syncthreads();
   best = sv[0];
@@ -86,9 +104,17 @@ __global__ __launch_bounds__(256) void heads_kernel(HeadsArgs a) {
   __syncthreads();
   if (tid == 0) {
     const float tot = (ssum[0] + ssum[1]) + (ssum[2] + ssum[3]);
-    a.top1[b] = best > -INFINITY ? best_i : -1;
-    a.max_logit[b] = best;
-    a.lse[b] = best > -INFINITY ? best + logf(tot) : -INFINITY;
+    if (nonfinite) {
+      int f = sfirst[0];
+      for (int i = 1; i < 4; ++i) f = sfirst[i] < f ? sfirst[i] : f;
+      a.top1[b] = f;
+      a.max_logit[b] = NAN;
+      a.lse[b] = NAN;
+    } else {
+      a.top1[b] = best > -INFINITY ? best_i : -1;
+      a.max_logit[b] = best;
+      a.lse[b] = best > -INFINITY ? best + logf(tot) : -INFINITY;
+    }
     float v = z[a.value_col], t = z[a.time_col];
     if (a.emulate_bf16) {
       v = round_bf16(tanhf(round_bf16(v)));

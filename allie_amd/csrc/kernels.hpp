@@ -240,6 +240,7 @@ struct HeadsArgs {
   const uint32_t* legal; // optional [B][legal_words] bitmask over move ids
   int legal_words;
   float* logits;         // [B][vocab] or null
+  float* logits_raw;     // [B][vocab] z before the bf16 rounding, or null
   float* value;          // [B]
   float* time;           // [B]
   int32_t* top1;         // [B]

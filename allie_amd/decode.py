@@ -20,8 +20,9 @@ for signature compatibility (the reference wraps calls in torch autocast,
 decode.py:74-78).
 
 Game rules (legal moves in python-chess order, game over) come from the
-native host rules (``allie_amd.rules``; ``allie_amd.movegen`` is their
-Python restatement) because python-chess is absent from this image.
+native host rules (``allie_amd.rules``; the tests check them against a
+Python restatement, oracle/movegen.py) because python-chess is absent from
+this image.
 The reference's quirks are kept: MCTS evaluates the root twice (:407, :410),
 and the "rating-based" sampling rule reads the Elo of the side to move
 (:97-107).
@@ -34,6 +35,32 @@ evaluated once.  ``leaf_batch=B`` (with ``kv_cache``) selects up to B leaves
 per round under virtual loss and evaluates them in one call, which is a
 different (batched) search.
 """
+# Portions of this file follow y0mingzhang/allie, src/evaluation/decode.py (the
+# decode strategies' API and search arithmetic), distributed under this
+# notice:
+#
+#   MIT License
+#
+#   Copyright (c) 2024 Yiming Zhang
+#
+#   Permission is hereby granted, free of charge, to any person obtaining a copy
+#   of this software and associated documentation files (the "Software"), to deal
+#   in the Software without restriction, including without limitation the rights
+#   to use, copy, modify, merge, publish, distribute, sublicense, and/or sell
+#   copies of the Software, and to permit persons to whom the Software is
+#   furnished to do so, subject to the following conditions:
+#
+#   The above copyright notice and this permission notice shall be included in all
+#   copies or substantial portions of the Software.
+#
+#   THE SOFTWARE IS PROVIDED "AS IS", WITHOUT WARRANTY OF ANY KIND, EXPRESS OR
+#   IMPLIED, INCLUDING BUT NOT LIMITED TO THE WARRANTIES OF MERCHANTABILITY,
+#   FITNESS FOR A PARTICULAR PURPOSE AND NONINFRINGEMENT. IN NO EVENT SHALL THE
+#   AUTHORS OR COPYRIGHT HOLDERS BE LIABLE FOR ANY CLAIM, DAMAGES OR OTHER
+#   LIABILITY, WHETHER IN AN ACTION OF CONTRACT, TORT OR OTHERWISE, ARISING FROM,
+#   OUT OF OR IN CONNECTION WITH THE SOFTWARE OR THE USE OR OTHER DEALINGS IN THE
+#   SOFTWARE.
+
 from __future__ import annotations
 
 import math

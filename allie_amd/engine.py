@@ -49,6 +49,21 @@ class PrefillResult:
     top1: torch.Tensor              # [B] int32
     max_logit: torch.Tensor         # [B]
     lse: torch.Tensor               # [B]
+    logits_raw: Optional[torch.Tensor] = None  # [B, vocab] fp32 before the bf16 rounding
+
+
+def _outputs(out: PrefillResult) -> "capi.AllieOutputs":
+    return capi.AllieOutputs(capi.ptr(out.logits).value, capi.ptr(out.value).value, capi.ptr(out.time).value,
+                             capi.ptr(out.top1).value, capi.ptr(out.max_logit).value, capi.ptr(out.lse).value,
+                             capi.ptr(out.logits_raw).value)
+
+
+def _new_result(n: int, vocab: int, dev, want_logits: bool, want_raw: bool) -> PrefillResult:
+    f = lambda: torch.empty(n, dtype=torch.float32, device=dev)
+    lg = lambda: torch.empty(n, vocab, dtype=torch.float32, device=dev)
+    return PrefillResult(logits=lg() if want_logits else None, value=f(), time=f(),
+                         top1=torch.empty(n, dtype=torch.int32, device=dev), max_logit=f(), lse=f(),
+                         logits_raw=lg() if want_raw else None)
 
 
 def _as_tensor(a) -> torch.Tensor:
@@ -132,7 +147,8 @@ class Engine:
     def prefill(self, words, lens, temperature: float = 1.0, legal=None, want_logits: bool = True,
                 kv_pool: Optional[torch.Tensor] = None, first_block: int = 0,
                 kv_block_table: Optional[torch.Tensor] = None,
-                out: Optional[PrefillResult] = None) -> PrefillResult:
+                out: Optional[PrefillResult] = None, want_raw_logits: bool = False,
+                status: Optional[torch.Tensor] = None) -> PrefillResult:
         """Forward of B games given as tokenizer words.
 
         words: uint32 words of all games back to back (numpy or a device
@@ -143,6 +159,9 @@ class Engine:
         layer's keys and values: game i's position p goes to block
         ``kv_block_table[i, p // 16]`` (device int32 [B, max_blocks]) if that
         table is given, else to the contiguous blocks from ``first_block``.
+        status: optional device int32 [1] that receives the packer's flags
+        (4: a game longer than its block-table row, 8: the <PAD> id inside a
+        game, which is then an ordinary token).
         """
         lens_np = np.ascontiguousarray(np.asarray(lens, dtype=np.int32))
         B = len(lens_np)
@@ -154,14 +173,8 @@ class Engine:
         n = np.minimum(lens_np, self.cfg.max_length)
         T = int(n.sum())
         if out is None:
-            f = lambda: torch.empty(B, dtype=torch.float32, device=dev)
-            out = PrefillResult(
-                logits=torch.empty(B, self.cfg.vocab_size, dtype=torch.float32, device=dev) if want_logits else None,
-                value=f(), time=f(), top1=torch.empty(B, dtype=torch.int32, device=dev),
-                max_logit=f(), lse=f(),
-            )
-        o = capi.AllieOutputs(capi.ptr(out.logits).value, capi.ptr(out.value).value, capi.ptr(out.time).value,
-                              capi.ptr(out.top1).value, capi.ptr(out.max_logit).value, capi.ptr(out.lse).value)
+            out = _new_result(B, self.cfg.vocab_size, dev, want_logits, want_raw_logits)
+        o = _outputs(out)
         ws_bytes = self.prefill_workspace_bytes(B, T)
         with torch.cuda.device(dev):
             ws = self._workspace(ws_bytes)
@@ -181,7 +194,7 @@ class Engine:
                 self._m, capi.ptr(wd), lens_np.ctypes.data_as(C.c_void_p), B, float(temperature),
                 capi.ptr(legal_t), LEGAL_WORDS if legal_t is not None else 0, C.byref(o),
                 capi.ptr(kv_pool), int(kv_blocks), int(first_block), capi.ptr(kv_block_table),
-                int(kv_max_blocks), capi.ptr(ws), ws.numel(), capi.stream_ptr(),
+                int(kv_max_blocks), capi.ptr(status), capi.ptr(ws), ws.numel(), capi.stream_ptr(),
             )
             capi.check(rc, "allie_prefill")
         return out
@@ -199,7 +212,7 @@ class Engine:
     def extend(self, ids, pos, group_sizes, prefix_len, prefix_blocks, extra_slot, n_extra,
                kv_pool: torch.Tensor, temperature: float = 1.0, legal=None, want_logits: bool = True,
                status: Optional[torch.Tensor] = None, out: Optional[PrefillResult] = None,
-               noalloc: bool = False) -> PrefillResult:
+               noalloc: bool = False, want_raw_logits: bool = False) -> PrefillResult:
         """Forward of n new tokens over the paged KV cache (decode steps, MCTS
         tree levels).  Tokens come in groups of ``group_sizes`` (host ints);
         token i of group g attends the group's prefix (``prefix_len[g]``
@@ -231,13 +244,8 @@ class Engine:
         ne_t = dt(n_extra)
         assert ids_t.numel() == n and pos_t.numel() == n and ne_t.numel() == n and pl_t.numel() == G
         if out is None:
-            f = lambda: torch.empty(n, dtype=torch.float32, device=dev)
-            out = PrefillResult(
-                logits=torch.empty(n, self.cfg.vocab_size, dtype=torch.float32, device=dev) if want_logits else None,
-                value=f(), time=f(), top1=torch.empty(n, dtype=torch.int32, device=dev), max_logit=f(), lse=f(),
-            )
-        o = capi.AllieOutputs(capi.ptr(out.logits).value, capi.ptr(out.value).value, capi.ptr(out.time).value,
-                              capi.ptr(out.top1).value, capi.ptr(out.max_logit).value, capi.ptr(out.lse).value)
+            out = _new_result(n, self.cfg.vocab_size, dev, want_logits, want_raw_logits)
+        o = _outputs(out)
         with torch.cuda.device(dev):
             legal_t = None
             if legal is not None:

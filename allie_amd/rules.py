@@ -3,16 +3,18 @@
 The search asks, per node, for the position after one more move, its legal
 moves in python-chess order and whether the game is over (the reference:
 src/modeling/data.py:51-61 and src/evaluation/decode.py:345-353, via
-python-chess).  ``NativeBoard`` answers these in C++; it has the methods of
-``allie_amd.movegen.Board`` that ``Game`` and the strategies use
-(``push_uci``, ``legal_uci``, ``outcome``, ``is_check``, ``is_game_over``),
-with the same results and move order.  The library is built by
-``allie_amd.build`` (``build()``), or on first use when it is missing; there
-is no switch to another implementation.
+python-chess).  ``NativeBoard`` answers these in C++ with the methods
+``Game`` and the strategies use (``push_uci``, ``legal_uci``, ``outcome``,
+``is_check``, ``is_game_over``); the tests compare it, move list for move
+list, with a Python restatement of the rules (oracle/movegen.py).  The
+library is built by ``allie_amd.build`` (``build()``), or on first use when
+it is missing or older than its sources; there is no switch to another
+implementation.
 """
 from __future__ import annotations
 
 import ctypes as C
+import glob
 import os
 import threading
 from typing import Optional
@@ -27,13 +29,23 @@ TERMINATIONS = {1: "checkmate", 2: "insufficient_material", 3: "stalemate", 4: "
 _WINNER = {0: None, 1: True, 2: False}
 
 
+def _stale() -> bool:
+    """The library is missing or older than one of its sources."""
+    if not os.path.exists(LIB_PATH):
+        return True
+    built = os.path.getmtime(LIB_PATH)
+    srcs = glob.glob(os.path.join(_HERE, "csrc", "*.cpp")) + [os.path.join(_HERE, "..", "include", "allie_chess.h")]
+    return any(os.path.exists(f) and os.path.getmtime(f) > built for f in srcs)
+
+
 def lib():
     global _lib
     if _lib is None:
         with _lock:
             if _lib is None:
-                if not os.path.exists(LIB_PATH):
-                    # host C++ only: built here on first use (g++, about two
+                if _stale():
+                    # host C++ only: built here on first use, or again when a
+                    # source is newer than the library (g++, about two
                     # seconds); a failed build raises
                     from .build import build_chess
 

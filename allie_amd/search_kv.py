@@ -49,6 +49,7 @@ class KVSearchCache:
         self.tok = tokenizer
         self.max_length = engine.cfg.max_length
         self.pool: Optional[torch.Tensor] = None
+        self.status: Optional[torch.Tensor] = None  # device int32 [1]: validation flags of the last call
         self.active = False
         self.n_evals = 0  # leaf evaluations made through extend (statistics)
 
@@ -75,13 +76,25 @@ class KVSearchCache:
         self.prefix_len = P
         self.table = torch.arange(pb, dtype=torch.int32, device=dev)[None].contiguous()
         self.next_slot = pb * KV_BLOCK
-        out = self.eng.prefill(words, np.array([P], np.int32), kv_pool=self.pool, kv_block_table=self.table)
+        if self.status is None:
+            self.status = torch.zeros(1, dtype=torch.int32, device=dev)
+        out = self.eng.prefill(words, np.array([P], np.int32), kv_pool=self.pool, kv_block_table=self.table,
+                               status=self.status)
         ev = NodeEval(out.logits[0].float().cpu(), float(out.value[0].item()), float(out.time[0].item()))
+        self._check_status("prefill")
         root._kv_path = []
         root._kv_eval = ev
         self.root = root
         self.active = True
         return ev
+
+    def _check_status(self, what: str) -> None:
+        """The device-side validation of the last call (read after its
+        outputs were copied, so it costs no extra synchronisation): a slot
+        or block outside the pool, a bad key count or position."""
+        st = int(self.status.item())
+        if st != 0:
+            raise RuntimeError(f"KV search {what} rejected its inputs on the device (status {st})")
 
     def end(self) -> None:
         self.active = False
@@ -121,10 +134,11 @@ class KVSearchCache:
             ids = np.array([n._kv_token for n in todo], np.int32)
             pos = (self.prefix_len + k - 1).astype(np.int32)
             out = self.eng.extend(ids, pos, [len(todo)], np.array([self.prefix_len], np.int32), self.table,
-                                  extras, k, self.pool)
+                                  extras, k, self.pool, status=self.status)
             logits = out.logits.float().cpu()
             value = out.value.cpu().tolist()
             time = out.time.cpu().tolist()
+            self._check_status("extend")
             for i, n in enumerate(todo):
                 n._kv_path = paths[i]
                 n._kv_eval = NodeEval(logits[i], value[i], time[i])

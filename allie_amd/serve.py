@@ -40,6 +40,7 @@ from .tokenizer import Game
 @dataclass
 class _Request:
     game: Game
+    legal: list
     future: Future
 
 
@@ -54,6 +55,7 @@ class PolicyBatcher:
         self.max_wait = max_wait_ms / 1000.0
         self._q: "queue.Queue[Optional[_Request]]" = queue.Queue()
         self._stop = False
+        self._lock = threading.Lock()  # orders submit's check-and-enqueue against close
         self.batches = 0
         self.requests = 0
         self._worker = threading.Thread(target=self._run, name="policy-batcher", daemon=True)
@@ -61,18 +63,31 @@ class PolicyBatcher:
 
     # -------------------------------------------------------------- callers
     def submit(self, game: Game) -> Future:
-        if self._stop:
-            raise RuntimeError("batcher is closed")
+        """Queue one game.  It is checked here, on the caller's thread, so a
+        bad request (an illegal move in its list, a missing Elo) fails only
+        its own future and never joins a shared forward."""
         f: Future = Future()
-        self._q.put(_Request(game, f))
+        try:
+            legal = game.legal_moves
+            self.strategy.tokenizer.tokenize(game)
+        except Exception as e:
+            f.set_exception(e)
+            return f
+        with self._lock:
+            if self._stop:
+                raise RuntimeError("batcher is closed")
+            self._q.put(_Request(game, legal, f))
         return f
 
     def decode_full(self, game: Game, timeout: Optional[float] = None) -> DecodeResult:
         return self.submit(game).result(timeout)
 
     def close(self) -> None:
-        self._stop = True
-        self._q.put(None)
+        with self._lock:
+            if self._stop:
+                return
+            self._stop = True
+            self._q.put(None)
         self._worker.join()
 
     # --------------------------------------------------------------- worker
@@ -96,7 +111,15 @@ class PolicyBatcher:
         while True:
             batch = self._take()
             if not batch:
-                return
+                # closed: nothing can be queued after the sentinel, but fail
+                # anything still waiting rather than leave it unresolved
+                while True:
+                    try:
+                        r = self._q.get_nowait()
+                    except queue.Empty:
+                        return
+                    if r is not None and not r.future.done():
+                        r.future.set_exception(RuntimeError("batcher is closed"))
             try:
                 self._serve(batch)
             except BaseException as e:  # every waiting caller sees the failure
@@ -107,7 +130,7 @@ class PolicyBatcher:
     def _serve(self, batch: list) -> None:
         st = self.strategy
         games = [r.game for r in batch]
-        legal = [g.legal_moves for g in games]
+        legal = [r.legal for r in batch]
         with torch.no_grad():
             out = st.model(**st.tokenizer.pad_and_collate(games))
         logits = out["logits"][:, -1].float().cpu()

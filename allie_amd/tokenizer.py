@@ -4,8 +4,9 @@ Mirrors ``Game`` (src/modeling/data.py:40-80) and ``UCITokenizer``
 (data.py:175-337) of the reference, with one difference forced by the image:
 python-chess is absent, so ``Game.legal_moves`` is taken from the caller
 (``Game(..., legal=[...])``) or from the native host rules
-(``allie_amd.rules``, restated in Python by ``allie_amd.movegen``).  The side to move is closed-form: white iff an even number of
-moves has been played, because every game starts from the initial position
+(``allie_amd.rules``; the tests' Python restatement is ``oracle/movegen.py``).
+The side to move is closed-form: white iff an even number of moves has been
+played, because every game starts from the initial position
 (data.py:51-56).
 
 ``UCITokenizer.tokenize`` produces the same uint32 words as data.py:217-270.
@@ -13,6 +14,32 @@ The GPU path consumes those words directly (``allie_amd.engine.Engine.prefill``
 takes ``words`` + ``lens``); ``pad_and_collate`` exists for the drop-in model
 call (data.py:281-337) and returns the same dict of padded tensors.
 """
+# Portions of this file follow y0mingzhang/allie, src/modeling/data.py (the
+# tokenizer's word format, padding and messages), distributed under this
+# notice:
+#
+#   MIT License
+#
+#   Copyright (c) 2024 Yiming Zhang
+#
+#   Permission is hereby granted, free of charge, to any person obtaining a copy
+#   of this software and associated documentation files (the "Software"), to deal
+#   in the Software without restriction, including without limitation the rights
+#   to use, copy, modify, merge, publish, distribute, sublicense, and/or sell
+#   copies of the Software, and to permit persons to whom the Software is
+#   furnished to do so, subject to the following conditions:
+#
+#   The above copyright notice and this permission notice shall be included in all
+#   copies or substantial portions of the Software.
+#
+#   THE SOFTWARE IS PROVIDED "AS IS", WITHOUT WARRANTY OF ANY KIND, EXPRESS OR
+#   IMPLIED, INCLUDING BUT NOT LIMITED TO THE WARRANTIES OF MERCHANTABILITY,
+#   FITNESS FOR A PARTICULAR PURPOSE AND NONINFRINGEMENT. IN NO EVENT SHALL THE
+#   AUTHORS OR COPYRIGHT HOLDERS BE LIABLE FOR ANY CLAIM, DAMAGES OR OTHER
+#   LIABILITY, WHETHER IN AN ACTION OF CONTRACT, TORT OR OTHERWISE, ARISING FROM,
+#   OUT OF OR IN CONNECTION WITH THE SOFTWARE OR THE USE OR OTHER DEALINGS IN THE
+#   SOFTWARE.
+
 from __future__ import annotations
 
 import logging

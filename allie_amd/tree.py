@@ -125,7 +125,8 @@ class TreeExpansion:
         wd = torch.from_numpy(words.view(np.int32)).to(self.eng.device)
         return self.eng.prefill(wd, lens, kv_pool=self.pool, kv_block_table=self.table, want_logits=False)
 
-    def expand_level(self, k: int, want_logits: bool = False, out=None):
+    def expand_level(self, k: int, want_logits: bool = False, out=None, want_raw_logits: bool = False):
         x = self.inputs[k - 1]
         return self.eng.extend(x["ids"], x["pos"], x["sizes"], x["prefix_len"], self.table, x["extras"],
-                               x["n_extra"], self.pool, want_logits=want_logits, status=self.status, out=out)
+                               x["n_extra"], self.pool, want_logits=want_logits, status=self.status, out=out,
+                               want_raw_logits=want_raw_logits)

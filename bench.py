@@ -95,41 +95,101 @@ def calibrate_copy(mib: int = 512, reps: int = 3):
     print(json.dumps({"calibration_copy_bytes": x.numel(), "reps": reps}), flush=True)
 
 
-def cpu_baseline(cfg, sd, seqs, budget_s: float = 20.0):
-    import torch
-
-    from oracle.model_ref import RefModel
-
-    cores = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(cores)
-    ref = RefModel(cfg, sd, mode="float32")
-    # one warm-up game, then B=1 forwards (as Policy.score_full calls the model)
-    ref.forward_padded(torch.as_tensor(seqs[0].astype(np.int64))[None])
-    done, t0 = 0, time.perf_counter()
-    for s in seqs:
-        ref.forward_padded(torch.as_tensor(s.astype(np.int64))[None])
-        done += 1
-        if time.perf_counter() - t0 > budget_s:
-            break
-    el = time.perf_counter() - t0
-    cpu_model = ""
+def _cpu_info():
+    model = ""
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
+                    model = line.split(":", 1)[1].strip()
                     break
     except OSError:
         pass
-    return {
-        "value": done / el,
-        "unit": "leaf evals/s",
-        "cores": cores,
+    return model
+
+
+def cpu_baseline(cfg, sd, leaves, unit, budget_s: float = 20.0, per_leaf: float = 1.0, extrapolate=None):
+    """The reference's CPU execution shape, timed on this host's cores: the
+    oracle in fp32 with all-position logits and no KV cache (the reference
+    model, src/modeling/model.py:85-147), over a fixed sample of ``leaves``
+    (token id sequences, each one evaluation the reference makes) in two
+    modes, each the median of 3 timed runs after one warm-up:
+
+    (i)  ``b1``: one B=1 forward per leaf, as Policy.score_full and
+         MCTS.evaluate_node call the model (src/evaluation/decode.py:199-203,
+         356-360) -- the reported ``value``;
+    (ii) ``padded``: the same leaves as ONE right-padded batch with an
+         attention mask, as pad_and_collate builds it (data.py:281-337).
+
+    The sample is the first leaves that fit the budget (about budget_s / 10
+    seconds per B=1 run; a padded run takes longer).  ``per_leaf`` converts leaves to the metric's unit
+    (e.g. tokens appended per leaf); ``extrapolate`` = (units, label) adds the
+    linear extrapolation of the B=1 rate to a whole workload.  Threads: the
+    cores this process may run on (its CPU affinity), which on a shared host
+    is the process's share rather than every core of the machine."""
+    import statistics
+
+    import torch
+
+    from oracle.model_ref import RefModel
+
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    torch.set_num_threads(avail)
+    ref = RefModel(cfg, sd, mode="float32")
+    fwd = lambda s: ref.forward_padded(torch.as_tensor(np.asarray(s, np.int64))[None])
+    fwd(leaves[0])  # warm-up
+    t0 = time.perf_counter()
+    fwd(leaves[0])
+    one = time.perf_counter() - t0
+    run_s = budget_s / 10.0
+    n = 1
+    est = one
+    while n < len(leaves) and est + one * len(leaves[n]) / max(len(leaves[0]), 1) < run_s:
+        est += one * len(leaves[n]) / max(len(leaves[0]), 1)
+        n += 1
+    sample = leaves[:n]
+
+    def b1():
+        t = time.perf_counter()
+        for s in sample:
+            fwd(s)
+        return time.perf_counter() - t
+
+    T = max(len(s) for s in sample)
+    ids = torch.full((n, T), 1996, dtype=torch.int64)
+    mask = torch.zeros(n, T)
+    for i, s in enumerate(sample):
+        ids[i, : len(s)] = torch.as_tensor(np.asarray(s, np.int64))
+        mask[i, : len(s)] = 1
+
+    def padded():
+        t = time.perf_counter()
+        ref.forward_padded(ids, mask)
+        return time.perf_counter() - t
+
+    modes = {}
+    b1()  # warm-up (the padded batch runs the same kernels)
+    for name, fn in (("b1", b1), ("padded", padded)):
+        runs = [fn() for _ in range(3)]
+        med = statistics.median(runs)
+        modes[name] = {"value": n * per_leaf / med, "runs_s": [round(r, 3) for r in runs]}
+    res = {
+        "value": modes["b1"]["value"],
+        "unit": unit,
+        "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"first {done} games of the same batch, one fp32 B=1 forward each "
-                  f"(all-position logits, no KV cache), {el:.1f} s; cpu {cpu_model!r}; "
-                  f"torch {torch.__version__}",
+        "sample": (f"{n} leaves of {min(len(s) for s in sample)}-{T} tokens; mode b1 (one fp32 B=1 forward "
+                   f"per leaf, all-position logits, no KV cache; the value) and mode padded (one right-padded "
+                   f"batch of them), each the median of 3 runs; os.cpu_count()={os.cpu_count()}, "
+                   f"affinity={avail}, torch threads={torch.get_num_threads()}; cpu {_cpu_info()!r}; "
+                   f"torch {torch.__version__}"),
+        "modes": modes,
     }
+    if extrapolate is not None:
+        units, label = extrapolate
+        res["extrapolated"] = {"workload": label, "seconds_at_b1_rate": units / modes["b1"]["value"],
+                               "note": "linear extrapolation of the timed sample"}
+    return res
 
 
 class Probe:
@@ -212,7 +272,8 @@ def bench_c2(args):
         args, config.MEDIUM, "bfloat16",
         "C2 ragged prefill: medium shape 24x1024x16, 256 prefixes, lens U[8,400] seed 2")
     eng.close()
-    res["cpu_baseline"] = None if args.no_cpu_baseline else cpu_baseline(config.MEDIUM, sd, seqs, args.cpu_budget)
+    res["cpu_baseline"] = None if args.no_cpu_baseline else cpu_baseline(
+        config.MEDIUM, sd, seqs, "leaf evals/s", args.cpu_budget, extrapolate=(len(seqs), "the 256-game C2 batch"))
     return res
 
 
@@ -239,7 +300,8 @@ def bench_c5(args):
     err = float((ob.logits - ref_logits).abs().max().item())
     bf.close()
     res["config"].update(top1_agreement_vs_bf16=agree, max_abs_logit_err_vs_bf16=err)
-    res["cpu_baseline"] = None
+    res["cpu_baseline"] = None if args.no_cpu_baseline else cpu_baseline(
+        cfg, sd, seqs, "leaf evals/s", args.cpu_budget, extrapolate=(len(seqs), "the 256-game C2 batch, 2x shape"))
     return res
 
 
@@ -253,7 +315,8 @@ def bench_c3(args):
 
     cfg = config.MEDIUM
     lay = TreeLayout(n_roots=64, prefix_len=200, branching=8, depth=4)
-    eng = Engine(cfg, weights.init_weights(cfg, seed=0), mode="bfloat16", device="cuda:0")
+    tx_sd = weights.init_weights(cfg, seed=0)
+    eng = Engine(cfg, tx_sd, mode="bfloat16", device="cuda:0")
     tx = TreeExpansion(eng, lay, seed=3)
     outs = [None] * lay.depth
 
@@ -307,8 +370,16 @@ def bench_c3(args):
                        "bound": "hbm", "achieved": a1["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": a1["achieved_GBs"] / HBM_PEAK_GBS, "traffic": read_traffic("c3_level1"),
                        "level2": dict(roof[2], traffic=read_traffic("c3_level2"))}
-    res["cpu_baseline"] = None
     eng.close()
+    res["cpu_baseline"] = None
+    if not args.no_cpu_baseline:
+        # the reference evaluates every leaf by a full recompute of its game
+        # (root prefix + ancestors + leaf), decode.py:356-360
+        from allie_amd.tree import node_path
+
+        paths = [node_path(lay, tx.prefixes, tx.levels, lay.depth, j) for j in range(0, leaves, 4097)]
+        res["cpu_baseline"] = cpu_baseline(cfg, tx_sd, paths, "leaf evals/s", args.cpu_budget,
+                                           extrapolate=(lay.level_size(lay.depth), "262,144 depth-4 leaves"))
     return res
 
 
@@ -321,7 +392,8 @@ def bench_c4(args):
     from allie_amd.engine import Engine
 
     cfg = config.MEDIUM
-    eng = Engine(cfg, weights.init_weights(cfg, seed=0), mode="bfloat16", device="cuda:0")
+    c4_sd = weights.init_weights(cfg, seed=0)
+    eng = Engine(cfg, c4_sd, mode="bfloat16", device="cuda:0")
     cb = ContinuousBatcher(eng, n_slots=args.slots)
     for _ in range(args.warmup):
         cb.step()
@@ -365,8 +437,24 @@ def bench_c4(args):
                        "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic("c4_decode"), "avg_launch_ms": att_ms,
                        "alg_bytes_per_launch": att_bytes}
-    res["cpu_baseline"] = None
     eng.close()
+    res["cpu_baseline"] = None
+    if not args.no_cpu_baseline:
+        # the reference appends a move with a full forward of the game so far
+        # (Policy.score_full, decode.py:199-203): leaves are the games of the
+        # same seeded queue at each length they pass through
+        from allie_amd.batcher import GameQueue
+
+        prefixes, P, total = GameQueue().draw(16)
+        rng = np.random.default_rng(0)
+        leaves = []
+        for p, tot in zip(prefixes, total):
+            g = list(p) + rng.integers(0, 1968, int(tot) - len(p)).tolist()
+            leaves += [g[:L] for L in range(len(p), int(tot), 16)]
+        order = np.random.default_rng(1).permutation(len(leaves))
+        leaves = [leaves[i] for i in order]
+        res["cpu_baseline"] = cpu_baseline(cfg, c4_sd, leaves, "tokens/s", args.cpu_budget,
+                                           extrapolate=(appended, f"the {args.steps} timed steps ({appended} moves)"))
     return res
 
 

@@ -123,7 +123,10 @@ int allie_pack_ragged(const uint32_t* words, const int32_t* lens, int n_seq, int
 
 /* Outputs of a forward, one entry per game (the values the decode
  * strategies read from out["logits"][:, -1], out["value_logits"][:, -1],
- * out["time_logits"][:, -1], decode.py:204-226). */
+ * out["time_logits"][:, -1], decode.py:204-226).  top1 follows the
+ * reference's argmax of softmax(logits / T) (decode.py:223-226): a NaN or
+ * +inf among the considered logits gives top1 = the first considered move
+ * id and max_logit = lse = NaN. */
 typedef struct allie_outputs {
   float* logits;     /* [n_seq][vocab] or NULL */
   float* value;      /* [n_seq] tanh value head */
@@ -131,6 +134,8 @@ typedef struct allie_outputs {
   int32_t* top1;     /* [n_seq] first argmax over (legal) move logits / T */
   float* max_logit;  /* [n_seq] that maximum (of logits / T) */
   float* lse;        /* [n_seq] logsumexp of (legal) move logits / T */
+  float* logits_raw; /* [n_seq][vocab] fp32 logits before the final bf16
+                        rounding of the bf16 modes, or NULL */
 } allie_outputs;
 
 /* Batched prefill forward: replaces `model(**pad_and_collate(games))` plus
@@ -142,13 +147,17 @@ typedef struct allie_outputs {
  * every layer's keys and values (NULL = no cache).  Game i's position p goes
  * to block kv_block_table[i][p / 16] (device int32 [n_seq][kv_max_blocks],
  * entries -1 or outside the pool are not written) when that table is given,
- * else to the contiguous blocks first_block + blk_off[i] ... */
+ * else to the contiguous blocks first_block + blk_off[i] ...
+ * status (device int32[1], optional) receives the packer's bitmask (see
+ * allie_pack_ragged): 4 a game longer than its kv_block_table row (its tail
+ * is not cached), 8 the <PAD> id inside a game (the reference's padded batch
+ * would mask that token, data.py:321; here it is an ordinary token). */
 size_t allie_prefill_workspace_bytes(const allie_model* m, int n_seq, int n_tokens);
 size_t allie_kv_block_bytes(const allie_model* m);
 int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_host, int n_seq,
                   float temperature, const uint32_t* legal, int legal_words,
                   const allie_outputs* out, void* kv_pool, int kv_pool_blocks, int first_block,
-                  const int32_t* kv_block_table, int kv_max_blocks,
+                  const int32_t* kv_block_table, int kv_max_blocks, int32_t* status,
                   void* workspace, size_t workspace_bytes, void* stream);
 
 /* Extend: the forward of n_tok NEW tokens over a paged KV cache -- one

@@ -13,7 +13,13 @@ Contents and what pins each part (details in each module's docstring):
   [lib] block arithmetic) in fp32 torch on the CPU, and a bf16-autocast
   emulation.  Pinned by a float64 numpy brute force at tiny shapes, by
   transformers' own GPT2LMHeadModel built from a local config with the same
-  weights, and by closed forms for the Elo control embedding.
-* ``decode_ref.py`` -- scalar maths of the decode strategies
-  (decode.py:194-238, 381-467, 503-516) used to check the host search code.
+  weights (fp32, and under torch.autocast for the bf16 mode), and by closed
+  forms for the Elo control embedding.
+* ``movegen.py`` -- the rules of chess in Python (python-chess's behaviour
+  behind data.py:51-61 and decode.py:345-353), the comparator of the native
+  rules library; legality pinned by perft known answers, move order
+  unpinned (python-chess is absent).
+
+The decode strategies' scalar maths (decode.py:381-467, 503-516) are checked
+in tests/test_decode.py against closed forms and a float64 bisection.
 """

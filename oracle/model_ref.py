@@ -63,9 +63,14 @@ def layer_norm(x: torch.Tensor, g: torch.Tensor, b: torch.Tensor, eps: float) ->
 
 
 class RefModel:
-    def __init__(self, cfg: ModelConfig, sd: dict, mode: str = "float32"):
+    """accumulate: "fp32", or "fp64" to sum every GEMM in float64 (rounding
+    points unchanged) -- an equally valid summation order, used to measure
+    how far two faithful bf16 implementations drift apart."""
+
+    def __init__(self, cfg: ModelConfig, sd: dict, mode: str = "float32", accumulate: str = "fp32"):
         assert mode in ("float32", "bfloat16", "fp8w")
-        self.cfg, self.mode = cfg, mode
+        assert accumulate in ("fp32", "fp64")
+        self.cfg, self.mode, self.acc64 = cfg, mode, accumulate == "fp64"
         t = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
         g = W.GLOBAL_KEYS
         self.wte, self.wpe, self.ctrl = t(sd[g["wte"]]), t(sd[g["wpe"]]), t(sd[g["ctrl"]])
@@ -83,22 +88,28 @@ class RefModel:
             self.layers.append(lw)
 
     # ---- numeric helpers -------------------------------------------------
+    def _mm(self, x, w):
+        if self.acc64:
+            return (x.double() @ w.double()).float()
+        return x @ w
+
     def _lin(self, x, w, b):
         """Conv1D / addmm (model weights are [in, out])."""
         if self.mode == "float32":
-            return x @ w + b
+            return self._mm(x, w) + b
         wq = w if self.mode == "fp8w" else rb(w)
-        return rb(rb(x) @ wq + rb(b))
+        return rb(self._mm(rb(x), wq) + rb(b))
 
-    def _lin_bf16(self, x, w, b):
+    def _lin_bf16(self, x, w, b, round_out=True):
         """Linear layers outside the blocks (heads): bf16 weights in both
-        reduced-precision modes."""
+        reduced-precision modes; round_out=False gives the fp32 result before
+        the output's bf16 rounding."""
         if self.mode == "float32":
-            return x @ w + (b if b is not None else 0.0)
-        y = rb(x) @ rb(w)
+            return self._mm(x, w) + (b if b is not None else 0.0)
+        y = self._mm(rb(x), rb(w))
         if b is not None:
             y = y + rb(b)
-        return rb(y)
+        return rb(y) if round_out else y
 
     # ---- pieces ------------------------------------------------------------
     def embed(self, ids: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
@@ -122,17 +133,17 @@ class RefModel:
         q = q.view(B, T, H, hd).transpose(1, 2)
         k = k.view(B, T, H, hd).transpose(1, 2)
         v = v.view(B, T, H, hd).transpose(1, 2)
-        s = (q @ k.transpose(-1, -2)) * (1.0 / math.sqrt(hd))
+        s = self._mm(q, k.transpose(-1, -2)) * (1.0 / math.sqrt(hd))
         causal = torch.ones(T, T, dtype=torch.bool).tril()
         allowed = causal[None, None] & key_mask[:, None, None, :]
         s = s.masked_fill(~allowed, float("-inf"))
         if self.mode == "float32":
             p = torch.softmax(s, dim=-1)
-            return (p @ v).transpose(1, 2).reshape(B, T, d)
+            return self._mm(p, v).transpose(1, 2).reshape(B, T, d)
         # bf16 SDPA: P = exp(s - rowmax) enters the PV product as bf16; the
         # row sum and the accumulation stay fp32
         p = torch.exp(s - s.max(dim=-1, keepdim=True).values)
-        o = (rb(p) @ v) / p.sum(dim=-1, keepdim=True)
+        o = self._mm(rb(p), v) / p.sum(dim=-1, keepdim=True)
         return rb(o.transpose(1, 2).reshape(B, T, d))
 
     def block(self, h: torch.Tensor, lw: dict, key_mask: torch.Tensor) -> torch.Tensor:
@@ -147,11 +158,12 @@ class RefModel:
 
     def heads(self, hL: torch.Tensor) -> dict:
         """hL: post-ln_f hidden state [..., d]."""
-        logits = self._lin_bf16(hL, self.wte.T, None)
+        raw = self._lin_bf16(hL, self.wte.T, None, round_out=False)
+        logits = raw if self.mode == "float32" else rb(raw)
         v = self._lin_bf16(hL, self.w_value.T, self.b_value)[..., 0]
         value = torch.tanh(v) if self.mode == "float32" else rb(torch.tanh(v))
         time = self._lin_bf16(hL, self.w_time.T, self.b_time)[..., 0]
-        return {"logits": logits, "value_logits": value, "time_logits": time}
+        return {"logits": logits, "value_logits": value, "time_logits": time, "logits_raw": raw}
 
     # ---- forwards ----------------------------------------------------------
     @torch.no_grad()
@@ -177,8 +189,9 @@ class RefModel:
     @torch.no_grad()
     def forward_last(self, seqs: list[np.ndarray], batch: int = 8) -> dict:
         """Last-token outputs of each id sequence (what Policy/MCTS read),
-        computed over right-padded sub-batches."""
-        outs = {"logits": [], "value_logits": [], "time_logits": []}
+        computed over right-padded sub-batches; ``logits_raw`` holds the
+        logits before their final bf16 rounding."""
+        outs = {"logits": [], "value_logits": [], "time_logits": [], "logits_raw": []}
         for i in range(0, len(seqs), batch):
             chunk = seqs[i : i + batch]
             T = max(len(s) for s in chunk)

@@ -1,4 +1,7 @@
-"""Host chess rules: legal moves, game over and outcome for ``Game``.
+"""Python restatement of the rules of chess -- TEST INFRASTRUCTURE ONLY.
+
+Only tests import it: it is the comparator of the native rules library
+(``allie_amd.rules``, csrc/chess.cpp) that ``Game`` uses.
 
 The reference gets these from python-chess (``Game.board`` replays the game
 with ``chess.Board().push_uci``, ``Game.legal_moves`` lists
@@ -6,9 +9,8 @@ with ``chess.Board().push_uci``, ``Game.legal_moves`` lists
 ``board.is_game_over()`` / ``board.outcome()``, src/evaluation/decode.py:
 345-353).  python-chess is not installed in this image, so this module
 restates the rules of chess for games that start from the initial position.
-``Game`` uses the native library with the same rules and order
-(``allie_amd.rules``, csrc/chess.cpp); this Python restatement is what the
-tests compare it with, move list for move list.
+The native library must give the same moves in the same order; the tests
+compare them move list for move list (tests/test_rules.py).
 
 Move ORDER matters to the reference: ``decode_full`` breaks argmax ties by
 the order of ``legal_moves`` (decode.py:112) and MCTS expands children in

@@ -20,7 +20,7 @@ def test_more_than_one_gpu_is_refused():
 def test_search_roots_are_legal_unfinished_games():
     sys.path.insert(0, ROOT)
     import bench
-    from allie_amd import movegen
+    from oracle import movegen
 
     games = bench.search_games(4, plies=30, seed=3)
     assert len(games) == 4

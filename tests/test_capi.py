@@ -81,3 +81,21 @@ def test_library_missing_raises(monkeypatch, tmp_path):
     monkeypatch.setattr(capi, "LIB_PATH", str(tmp_path / "nope.so"))
     with pytest.raises(capi.AllieError):
         capi.lib()
+
+
+def test_gemm_split_factor_of_decode_shapes():
+    """The K splits the forward picks for small-M projections (a host
+    function; no GPU needed): unsplit at K = 1024 once M fills the CUs,
+    more splits the fewer rows there are."""
+    if not os.path.exists(capi.LIB_PATH):
+        pytest.skip("library not built (run __graft_entry__.build())")
+    f = capi.lib().allie_gemm_split_factor
+    assert f(63, 1024, 4096) == 8    # decode-step MLP c_proj, 63 rows
+    assert f(63, 3072, 1024) == 4    # decode-step QKV
+    assert f(1024, 1024, 4096) == 4
+    assert f(1450, 1024, 4096) == 2  # C4 step (about 1,450 rows)
+    assert f(1450, 3072, 1024) == 1
+    for M in (1, 8, 64, 256, 1450, 53205):
+        for N, K in ((3072, 1024), (1024, 1024), (4096, 1024), (1024, 4096)):
+            s = f(M, N, K)
+            assert s >= 1 and (K // 32) % s == 0

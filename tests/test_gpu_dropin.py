@@ -59,13 +59,24 @@ def test_model_call_matches_reference_shape(models):
     assert got["logits"].shape == (5, 1, cfg.vocab_size) and got["value_logits"].shape == (5, 1)
 
 
-@pytest.mark.parametrize("name,kw", [("policy", {"temperature": 0.5}), ("mcts", {"n_sims": 16}),
-                                     ("adaptive-mcts", {"mean_n_sims": 10})])
-def test_strategies_same_decisions(models, name, kw):
+# gpu_kw: options of the GPU strategy only.  kv_cache=True evaluates each
+# search leaf as one token over the root's cached keys (sequential, root
+# evaluated once); its decisions must equal the oracle-driven search that
+# recomputes every leaf's whole game, as MCTS.evaluate_node does
+# (src/evaluation/decode.py:356-373, 401-467, 575-658).
+@pytest.mark.parametrize("name,kw,gpu_kw", [
+    ("policy", {"temperature": 0.5}, {}),
+    ("mcts", {"n_sims": 16}, {}),
+    ("adaptive-mcts", {"mean_n_sims": 10}, {}),
+    ("mcts", {"n_sims": 16}, {"kv_cache": True}),
+    ("mcts", {"n_sims": 16}, {"kv_cache": True, "leaf_batch": 1}),
+    ("adaptive-mcts", {"mean_n_sims": 10}, {"kv_cache": True}),
+])
+def test_strategies_same_decisions(models, name, kw, gpu_kw):
     gpu, ora, _, _ = models
     tok = UCITokenizer(max_length=512)
     for g in games()[1:4]:
-        a = DECODE_STRATEGIES[name](gpu, tok, device="cuda", **kw)
+        a = DECODE_STRATEGIES[name](gpu, tok, device="cuda", **kw, **gpu_kw)
         b = DECODE_STRATEGIES[name](ora, tok, device="cpu", **kw)
         ra = a.score_full(g, g.legal_moves)
         rb = b.score_full(g, g.legal_moves)
@@ -73,7 +84,10 @@ def test_strategies_same_decisions(models, name, kw):
                                    atol=1e-3)
         assert a.decode_full(g).move == b.decode_full(g).move
         if name != "policy":
-            assert a.run_stats() == b.run_stats()
+            sa, sb = a.run_stats(), b.run_stats()
+            assert sa["total_rollouts"] == sb["total_rollouts"]
+            if gpu_kw.get("kv_cache"):
+                assert sa["kv_leaf_evaluations"] > 0
 
 
 def test_bf16_model_plays(cuda):

@@ -203,10 +203,11 @@ def _gemm_split(A, Wt, bias, epi, wtype, split, out_f32=False, R=None, scale=Non
     return C_
 
 
-# (M, N, K, split): 0 = the forward's own choice (8 for the decode-step MLP
-# c_proj), ragged last m-tile, the heads' fp32 output
-SPLIT_CASES = [(1024, 1024, 4096, 0), (300, 3072, 1024, 4), (1000, 1024, 1024, 2), (256, 2048, 1024, 4),
-               (77, 512, 2048, 16)]
+# (M, N, K, split): 0 = the forward's own choice (4 at M = 1024 and 8 at
+# M = 63 for the MLP c_proj, see test_capi.py), ragged last m-tile, the
+# heads' fp32 output
+SPLIT_CASES = [(1024, 1024, 4096, 0), (63, 1024, 4096, 0), (300, 3072, 1024, 4), (1000, 1024, 1024, 2),
+               (256, 2048, 1024, 4), (77, 512, 2048, 16)]
 
 
 @pytest.mark.parametrize("M,N,K,split", SPLIT_CASES)

@@ -1,4 +1,4 @@
-"""Host chess rules (allie_amd/movegen.py): legality pinned by perft known
+"""Python chess rules restatement (oracle/movegen.py): legality pinned by perft known
 answers (node counts of the legal-move tree; the standard test positions of
 the chess-programming literature exercise castling through and out of check,
 en passant with pins and discovered checks, and under-promotion), plus
@@ -8,7 +8,7 @@ import time
 
 import pytest
 
-from allie_amd.movegen import Board, board_after, legal_moves, perft
+from oracle.movegen import Board, board_after, legal_moves, perft
 
 KIWIPETE = "r3k2r/p1ppqpb1/bn2pnp1/3PN3/1p2P3/2N2Q1p/PPPBBPPP/R3K2R w KQkq - 0 1"
 POS3 = "8/2p5/3p4/KP5r/1R3p1k/8/4P1P1/8 w - - 0 1"

@@ -3,7 +3,7 @@
 * Legality: perft known answers of the standard test positions (deeper than
   the Python restatement's test can afford).
 * Order and game over: the same legal-move lists, in the same order, and the
-  same outcomes as allie_amd/movegen.py on every position of seeded random
+  same outcomes as oracle/movegen.py on every position of seeded random
   games and of the test positions' subtrees (the order itself follows
   python-chess's generation order, unpinned without python-chess).
 * Outcome known answers: mate, stalemate, insufficient material, the
@@ -12,7 +12,7 @@
 import numpy as np
 import pytest
 
-from allie_amd import movegen
+from oracle import movegen
 from allie_amd.rules import NativeBoard, board_after
 
 KIWIPETE = "r3k2r/p1ppqpb1/bn2pnp1/3PN3/1p2P3/2N2Q1p/PPPBBPPP/R3K2R w KQkq - 0 1"

@@ -146,3 +146,55 @@ def test_model_failure_reaches_every_caller():
         b.submit(games()[0])
     with pytest.raises(TypeError):
         PolicyBatcher(DECODE_STRATEGIES["mcts"](Broken(), tok, device="cpu"))
+
+
+def test_bad_request_fails_alone(model):
+    """A request with an illegal move, or no Elo for the tokenizer, fails its
+    own future on submit; the good requests around it are still answered
+    from one shared forward."""
+    tok = UCITokenizer(max_length=512)
+    seq = DECODE_STRATEGIES["policy"](model, tok, device="cpu")
+    b = PolicyBatcher(DECODE_STRATEGIES["policy"](model, tok, device="cpu"), max_batch=8, max_wait_ms=200)
+    try:
+        good = games()[1:5]
+        illegal = Game("300+0", 1500, 1500, None, False, ["e2e4", "e2e4"], [3, 3], None)
+        no_elo = Game("300+0", None, 1500, None, False, ["e2e4"], [3], None)
+        fs = [b.submit(good[0]), b.submit(illegal), b.submit(good[1]), b.submit(no_elo),
+              b.submit(good[2]), b.submit(good[3])]
+        with pytest.raises(Exception):
+            fs[1].result(timeout=30)
+        with pytest.raises(Exception):
+            fs[3].result(timeout=30)
+        got = [fs[i].result(timeout=60) for i in (0, 2, 4, 5)]
+    finally:
+        b.close()
+    assert [g.move for g in got] == [seq.decode_full(g).move for g in good]
+    assert b.requests == 4
+
+
+def test_close_resolves_every_future(model):
+    """Submitting races close: every submit either raises or gets a future
+    that resolves (no caller waits forever)."""
+    tok = UCITokenizer(max_length=512)
+    b = PolicyBatcher(DECODE_STRATEGIES["policy"](model, tok, device="cpu"), max_batch=4, max_wait_ms=1)
+    futs, errors = [], []
+
+    def spam():
+        for g in games() * 3:
+            try:
+                futs.append(b.submit(g))
+            except RuntimeError:
+                errors.append(1)
+
+    ts = [threading.Thread(target=spam) for _ in range(3)]
+    for t in ts:
+        t.start()
+    b.close()
+    for t in ts:
+        t.join()
+    for f in futs:
+        try:
+            f.result(timeout=60)
+        except RuntimeError:
+            pass
+    assert all(f.done() for f in futs)
