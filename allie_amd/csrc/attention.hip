@@ -316,7 +316,7 @@ __global__ __launch_bounds__(256) void kv_write_kernel(KVWriteArgs a) {
   for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
     const int e = c * per_chunk;                 // element in [0, 2d): kv * d + head * hd + i
     const int kvi = e / d, rem = e - kvi * d, head = rem / hd, i = rem - head * hd;
-    const int64_t dst = ((((blk * a.n_layer + a.layer) * 2 + kvi) * H + head) * KV_BLOCK + off) * hd + i;
+    const int64_t dst = (((((int64_t)a.layer * a.pool_blocks + blk) * 2 + kvi) * H + head) * KV_BLOCK + off) * hd + i;
     *reinterpret_cast<uint4*>(reinterpret_cast<char*>(a.pool) + dst * esz) =
         *reinterpret_cast<const uint4*>(src + (int64_t)e * esz);
   }

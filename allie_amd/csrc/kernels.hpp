@@ -149,7 +149,7 @@ hipError_t launch_attn_varlen(const AttnVarlenArgs& a, hipStream_t st);
 
 // Paged attention: queries are new tokens of B sequences; keys/values come
 // from a paged pool (block = 16 tokens) that already holds the new tokens.
-// Pool layout: [block][layer][k|v][head][16][head_dim]; slot = block*16 + offset.
+// Pool layout: [layer][pool_blocks][k|v][head][16][head_dim]; slot = block*16 + offset.
 constexpr int KV_BLOCK = 16;
 struct KVWriteArgs {
   const void* qkv;       // [T][3d]
@@ -168,7 +168,7 @@ hipError_t launch_kv_write(const KVWriteArgs& a, hipStream_t st);
 //   2. its private keys: the n_extra[i] pool slots extra_slot[i][0 ..] (a
 //      search node's ancestors, then the token itself).
 // Every key is visible (the causal order is in how the caller builds the
-// lists).  Pool layout: [block][layer][k|v][head][16][head_dim].  Block ids
+// lists).  Pool layout: [layer][pool_blocks][k|v][head][16][head_dim].  Block ids
 // and slots outside the pool are skipped (and flagged by extend_prepare).
 struct ExtendAttnArgs {
   const void* qkv;             // [n][3d] new tokens (q | k | v)

@@ -202,7 +202,7 @@ class Engine:
     # ------------------------------------------------------------- KV cache
     def new_kv_pool(self, n_blocks: int) -> torch.Tensor:
         """Device KV pool of n_blocks blocks of 16 positions (every layer's
-        keys and values, layout [block][layer][k|v][head][16][64])."""
+        keys and values, layout [layer][block][k|v][head][16][64])."""
         return torch.empty(n_blocks * self.kv_block_bytes(), dtype=torch.uint8, device=self.device)
 
     def pool_blocks(self, kv_pool: torch.Tensor) -> int:

@@ -143,7 +143,9 @@ typedef struct allie_outputs {
  * words: device word stream; lens_host: host array [n_seq].
  * legal: optional [n_seq][legal_words] bitmask over move ids (NULL = all).
  * kv_pool: optional paged KV pool of kv_pool_blocks blocks (layout
- * [block][layer][k|v][head][16][head_dim], activation dtype) that receives
+ * [layer][kv_pool_blocks][k|v][head][16][head_dim], activation dtype; the
+ * layout depends on the block count, so every call on one pool must pass the
+ * same kv_pool_blocks, its true size) that receives
  * every layer's keys and values (NULL = no cache).  Game i's position p goes
  * to block kv_block_table[i][p / 16] (device int32 [n_seq][kv_max_blocks],
  * entries -1 or outside the pool are not written) when that table is given,
