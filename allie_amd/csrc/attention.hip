@@ -209,12 +209,13 @@ __global__ __launch_bounds__(SEQ_WAVES * 64, 1) void attn_varlen_seq_kernel(Attn
   // order; then every wave is done with the staged head and the next one
   // (loaded meanwhile) takes its place
   const int T32 = npad / 32;
+  const int n_run = a.last_only ? 1 : T32;  // last_only: the tile holding the last query
   for (int head = h_first; head < h_end; ++head) {
     const bool more = head + 1 < h_end;
     if (more) load_head(head + 1);
-    for (int r = 0; r * SEQ_WAVES < T32; ++r) {
+    for (int r = 0; r * SEQ_WAVES < n_run; ++r) {
       const int idx = r * SEQ_WAVES + ((r & 1) ? SEQ_WAVES - 1 - wave : wave);
-      if (idx < T32) tile(head, T32 - 1 - idx);
+      if (idx < n_run) tile(head, T32 - 1 - idx);
     }
     if (!more) break;
     __syncthreads();

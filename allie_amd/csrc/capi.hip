@@ -230,6 +230,10 @@ size_t part_bytes(const allie_model* m, int T, int heads_rows) {
   need(T, 4 * d, d);
   need(T, d, 4 * d);
   need(heads_rows, m->NH, d);
+  // a prefill's last block on the games' last rows
+  need(heads_rows, d, d);
+  need(heads_rows, 4 * d, d);
+  need(heads_rows, d, 4 * d);
   return mx;
 }
 
@@ -342,6 +346,20 @@ bool store_is_persistent(const allie_model* m, int M, int N, int K, const float*
   return gemm_uses_persistent(g);
 }
 
+// Rows the last block is finished on when only some rows' outputs are read
+// (the heads of a prefill read each game's last token): the last block's
+// attention runs over all rows (its keys and values are every row's), then
+// its output rows idx[0..n) and their residual rows move into these compact
+// buffers and the rest of the block (c_proj, ln_2, MLP) runs on n rows.
+struct Compact {
+  const int32_t* idx;
+  int n;
+  void* attn;  // [n][d] activations
+  void* x;     // [n][d]
+  float* h;    // [n][d] fp32
+  void* ff;    // [n][4d]
+};
+
 // The transformer blocks over T rows whose embeddings (h) and first ln_1 (x)
 // are in place.  kv_slot/kv_pool: every layer's keys and values of row t are
 // written to pool slot kv_slot[t] (before attention runs).  attn(layer) runs
@@ -351,23 +369,59 @@ bool store_is_persistent(const allie_model* m, int M, int N, int K, const float*
 // h += bf16(y + b) (src/modeling/model.py:50-55 -> [lib] GPT2Block).  Small-M
 // GEMMs add into h in their epilogue; GEMMs on the persistent kernel store y
 // (bf16, into x) and the next LayerNorm adds it (h += y; x = LN(h)).  After
-// the last block, *final_add is the y still to be added to h (the heads'
-// ln_f adds it on the rows it reads), or null.
+// the last block, *h_final is the residual stream the heads read (acts.h, or
+// cp->h when cp finishes the last block on cp->n rows) and *final_add the y
+// still to be added to it (the heads' ln_f adds it on the rows it reads), or
+// null.
 template <typename AttnFn>
 int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slot, void* kv_pool,
-               int kv_pool_blocks, AttnFn&& attn, hipStream_t st, const void** final_add) {
+               int kv_pool_blocks, AttnFn&& attn, hipStream_t st, const Compact* cp, const float** h_final,
+               const void** final_add) {
   const int d = m->d, L = m->L, act = m->act_bf16;
-  LNArgs ln{};
-  ln.h = w.h;
-  ln.rows = ln.rows_out = T;
-  ln.d = d;
-  ln.eps = m->cfg.eps;
-  ln.y = w.x;
-  ln.act_bf16 = act;
-  const bool fuse_proj = store_is_persistent(m, T, d, d, w.part, w.wdq);
-  const bool fuse_fc2 = store_is_persistent(m, T, d, 4 * d, w.part, w.wdq);
   *final_add = nullptr;
+  *h_final = w.h;
   int rc;
+  // c_proj, ln_2 and the MLP of layer li over M rows (attention output in
+  // attn, residual stream h), then the next layer's ln_1 into x
+  auto finish = [&](int li, int M, void* attn_in, void* x, float* h, void* ff) -> int {
+    const LayerW& l = m->layers[li];
+    const bool fuse_proj = store_is_persistent(m, M, d, d, w.part, w.wdq);
+    const bool fuse_fc2 = store_is_persistent(m, M, d, 4 * d, w.part, w.wdq);
+    LNArgs ln{};
+    ln.h = h;
+    ln.rows = ln.rows_out = M;
+    ln.d = d;
+    ln.eps = m->cfg.eps;
+    ln.y = x;
+    ln.act_bf16 = act;
+    int r;
+    if (fuse_proj) {
+      if ((r = gemm(m, attn_in, l.w_o, l.b_o, l.s_o, x, nullptr, M, d, d, EPI_STORE, ALLIE_PROBE_PROJ, w.part, w.wdq, st))) return r;
+    } else {
+      if ((r = gemm(m, attn_in, l.w_o, l.b_o, l.s_o, nullptr, h, M, d, d, EPI_RESID, ALLIE_PROBE_PROJ, w.part, w.wdq, st))) return r;
+    }
+    ln.g = l.ln2_g;
+    ln.b = l.ln2_b;
+    ln.add = fuse_proj ? x : nullptr;
+    ln.h_out = fuse_proj ? h : nullptr;
+    HIP_TRY(launch_layernorm(ln, st));
+    if ((r = gemm(m, x, l.w_fc, l.b_fc, l.s_fc, ff, nullptr, M, 4 * d, d, EPI_GELU, ALLIE_PROBE_FC, w.part, w.wdq, st))) return r;
+    if (fuse_fc2) {
+      if ((r = gemm(m, ff, l.w_pr, l.b_pr, l.s_pr, x, nullptr, M, d, 4 * d, EPI_STORE, ALLIE_PROBE_FC2, w.part, w.wdq, st))) return r;
+    } else {
+      if ((r = gemm(m, ff, l.w_pr, l.b_pr, l.s_pr, nullptr, h, M, d, 4 * d, EPI_RESID, ALLIE_PROBE_FC2, w.part, w.wdq, st))) return r;
+    }
+    if (li + 1 < L) {
+      ln.g = m->layers[li + 1].ln1_g;
+      ln.b = m->layers[li + 1].ln1_b;
+      ln.add = fuse_fc2 ? x : nullptr;
+      ln.h_out = fuse_fc2 ? h : nullptr;
+      HIP_TRY(launch_layernorm(ln, st));
+    } else {
+      *final_add = fuse_fc2 ? x : nullptr;
+    }
+    return ALLIE_OK;
+  };
   for (int li = 0; li < L; ++li) {
     const LayerW& l = m->layers[li];
     if ((rc = gemm(m, w.x, l.w_qkv, l.b_qkv, l.s_qkv, w.qkv, nullptr, T, 3 * d, d, EPI_STORE, ALLIE_PROBE_QKV, w.part, w.wdq, st))) return rc;
@@ -386,31 +440,15 @@ int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slo
       HIP_TRY(launch_kv_write(kw, st));
     }
     if ((rc = attn(li))) return rc;
-    if (fuse_proj) {
-      if ((rc = gemm(m, w.attn, l.w_o, l.b_o, l.s_o, w.x, nullptr, T, d, d, EPI_STORE, ALLIE_PROBE_PROJ, w.part, w.wdq, st))) return rc;
-    } else {
-      if ((rc = gemm(m, w.attn, l.w_o, l.b_o, l.s_o, nullptr, w.h, T, d, d, EPI_RESID, ALLIE_PROBE_PROJ, w.part, w.wdq, st))) return rc;
+    if (li + 1 == L && cp) {
+      // the residual stream is current here: the last ln_1 wrote back its add
+      const int a = act ? 2 : 4;
+      HIP_TRY(launch_gather_rows(w.attn, cp->idx, cp->n, d * a, cp->attn, st));
+      HIP_TRY(launch_gather_rows(w.h, cp->idx, cp->n, d * 4, cp->h, st));
+      *h_final = cp->h;
+      return finish(li, cp->n, cp->attn, cp->x, cp->h, cp->ff);
     }
-    ln.g = l.ln2_g;
-    ln.b = l.ln2_b;
-    ln.add = fuse_proj ? w.x : nullptr;
-    ln.h_out = fuse_proj ? w.h : nullptr;
-    HIP_TRY(launch_layernorm(ln, st));
-    if ((rc = gemm(m, w.x, l.w_fc, l.b_fc, l.s_fc, w.ff, nullptr, T, 4 * d, d, EPI_GELU, ALLIE_PROBE_FC, w.part, w.wdq, st))) return rc;
-    if (fuse_fc2) {
-      if ((rc = gemm(m, w.ff, l.w_pr, l.b_pr, l.s_pr, w.x, nullptr, T, d, 4 * d, EPI_STORE, ALLIE_PROBE_FC2, w.part, w.wdq, st))) return rc;
-    } else {
-      if ((rc = gemm(m, w.ff, l.w_pr, l.b_pr, l.s_pr, nullptr, w.h, T, d, 4 * d, EPI_RESID, ALLIE_PROBE_FC2, w.part, w.wdq, st))) return rc;
-    }
-    if (li + 1 < L) {
-      ln.g = m->layers[li + 1].ln1_g;
-      ln.b = m->layers[li + 1].ln1_b;
-      ln.add = fuse_fc2 ? w.x : nullptr;
-      ln.h_out = fuse_fc2 ? w.h : nullptr;
-      HIP_TRY(launch_layernorm(ln, st));
-    } else if (fuse_fc2) {
-      *final_add = w.x;
-    }
+    if ((rc = finish(li, T, w.attn, w.x, w.h, w.ff))) return rc;
   }
   return ALLIE_OK;
 }
@@ -851,19 +889,37 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
   aa.act_bf16 = act;
 
   const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff, w.part, w.wdq};
+  // Only each game's last token reaches the heads, so the last block's c_proj,
+  // ln_2 and MLP run on those n_seq rows (when they are at most half the
+  // tokens): its attention output and residual rows are gathered into x
+  // (free once the block's QKV has read it) and ff (not yet written).
+  Compact cp{};
+  const bool compact = 2 * (int64_t)n_seq <= T;
+  if (compact) {
+    const size_t a = act ? 2 : 4;
+    cp.idx = w.last;
+    cp.n = n_seq;
+    cp.attn = w.x;
+    cp.x = (char*)w.x + align_up((size_t)n_seq * d * a);
+    cp.h = (float*)w.ff;
+    cp.ff = (char*)w.ff + align_up((size_t)n_seq * d * 4);
+  }
   const void* final_add = nullptr;
+  const float* h_final = nullptr;
   rc = run_layers(m, acts, (int)T, kv_pool ? w.slot : nullptr, kv_pool, kv_pool_blocks,
                   [&](int layer) -> int {
                     HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, true, st));
                     aa.order_ready = layer > 0;  // the game order is computed once per forward
+                    aa.last_only = compact && layer == L - 1;  // only the compact rows are read
                     HIP_TRY(launch_attn_varlen(aa, st));
                     HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, false, st));
                     return ALLIE_OK;
                   },
-                  st, &final_add);
+                  st, compact ? &cp : nullptr, &h_final, &final_add);
   if (rc) return rc;
-  // heads on the last token of every game
-  return run_heads(m, w.h, final_add, w.last, n_seq, w.hx, w.z, temperature, legal, legal_words, out, w.part, st);
+  // heads on the last token of every game (row b of the compact rows is game b's)
+  return run_heads(m, h_final, final_add, compact ? nullptr : w.last, n_seq, w.hx, w.z, temperature, legal,
+                   legal_words, out, w.part, st);
 }
 
 size_t allie_extend_workspace_bytes(const allie_model* m, int n_tok, int n_groups) {
@@ -1013,6 +1069,7 @@ int extend_run(allie_model* m, const ExtendPlan& plan, const ExtendWS& w, const 
   };
   const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff, w.part, w.wdq};
   const void* final_add = nullptr;
+  const float* h_final = nullptr;
   rc = run_layers(m, acts, n_tok, w.self_slot, kv_pool, kv_pool_blocks,
                   [&](int layer) -> int {
                     xa.layer = layer;
@@ -1037,7 +1094,7 @@ int extend_run(allie_model* m, const ExtendPlan& plan, const ExtendWS& w, const 
                     }
                     return ALLIE_OK;
                   },
-                  st, &final_add);
+                  st, nullptr, &h_final, &final_add);
   if (rc) return rc;
   return run_heads(m, w.h, final_add, nullptr, n_tok, w.hx, w.z, temperature, legal, legal_words, out, w.part, st);
 }

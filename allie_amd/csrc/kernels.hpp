@@ -143,6 +143,8 @@ struct AttnVarlenArgs {
   int act_bf16;
   int32_t* order;        // bf16 path: [B] workspace, games by decreasing length
   int order_ready;       // order already holds this batch's order (later layers)
+  int last_only;         // bf16 path: only each game's last row of out is needed (the
+                         // other rows may be left unwritten)
 };
 constexpr int ATTN_Q_TILE = 64;
 hipError_t launch_attn_varlen(const AttnVarlenArgs& a, hipStream_t st);
@@ -256,5 +258,9 @@ hipError_t launch_transpose_convert(const float* src, int rows, int cols, void* 
                                     int ld_dst, hipStream_t st);
 hipError_t launch_convert(const float* src, int64_t n, void* dst, int dst_bf16, int round_bf16,
                           hipStream_t st);
+
+// dst row r = src row idx[r] (rows of row_bytes, a multiple of 16)
+hipError_t launch_gather_rows(const void* src, const int32_t* idx, int rows, int row_bytes, void* dst,
+                              hipStream_t st);
 
 }  // namespace allie

@@ -147,6 +147,15 @@ __global__ __launch_bounds__(256) void layernorm_kernel(allie::LNArgs a) {
   ln_row_store<NV>(v, d, a.g, a.b, a.eps, a.y, r, a.act_bf16);
 }
 
+// dst row r = src row idx[r], 16 bytes per thread
+__global__ __launch_bounds__(256) void gather_rows_kernel(const char* __restrict__ src, const int32_t* __restrict__ idx,
+                                                          int row_bytes, char* __restrict__ dst) {
+  const int64_t r = blockIdx.x;
+  const int64_t s = idx[r];
+  for (int c = threadIdx.x * 16; c < row_bytes; c += 256 * 16)
+    *reinterpret_cast<uint4*>(dst + r * row_bytes + c) = *reinterpret_cast<const uint4*>(src + s * row_bytes + c);
+}
+
 __global__ void transpose_convert_kernel(const float* __restrict__ src, int rows, int cols,
                                          void* dst, int dst_bf16, int ld_dst) {
   // src [rows][cols] -> dst[c][r] (ld_dst = row stride of dst)
@@ -212,6 +221,15 @@ hipError_t launch_layernorm(const LNArgs& a, hipStream_t st) {
   if (a.rows_out == 0) return hipSuccess;
   dim3 grid((a.rows_out + 3) / 4);
   ALLIE_NV_SWITCH(a.d / 256, hipLaunchKernelGGL(layernorm_kernel<NV>, grid, dim3(256), 0, st, a));
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(const void* src, const int32_t* idx, int rows, int row_bytes, void* dst,
+                              hipStream_t st) {
+  if (row_bytes % 16 != 0 || rows < 0) return hipErrorInvalidValue;
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)rows), dim3(256), 0, st, static_cast<const char*>(src), idx,
+                     row_bytes, static_cast<char*>(dst));
   return hipGetLastError();
 }
 

@@ -93,6 +93,23 @@ def test_prefill_tiny_large_batch(tiny, mode, cuda):
     eng.close()
 
 
+@pytest.mark.parametrize("mode,tol", [("float32", 1e-4), ("bfloat16", 2e-2)])
+@pytest.mark.parametrize("lo,hi", [(1, 2), (20, 60)])
+def test_prefill_last_block_rows(tiny, mode, tol, lo, hi, cuda):
+    """The heads read each game's last token only, so the last block's
+    c_proj, ln_2 and MLP run on those rows when the games hold at least twice
+    as many tokens as there are games (lengths 20..60), and on every row
+    otherwise (lengths 1..2); both against the oracle's full forward."""
+    cfg, sd = tiny
+    seqs, lens = synth_games(11, 40, lo, hi)
+    assert (2 * len(lens) <= lens.sum()) == (lo >= 20)
+    eng = Engine(cfg, sd, mode=mode)
+    got = run_engine(eng, seqs, lens)
+    ref = RefModel(cfg, sd, mode=mode).forward_last([(s & 0x3FFF).astype(np.int64) for s in seqs])
+    check(got, ref, tol, f"{mode}-lens{lo}-{hi}")
+    eng.close()
+
+
 def test_prefill_legal_mask_and_temperature(tiny, cuda):
     cfg, sd = tiny
     seqs, lens = synth_games(3, 9, 5, 60)
