@@ -143,6 +143,9 @@ ALLIE_DEV u32x4_t fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
 // output of the MFMA kernel: bf16 through LDS, fp32 rows (heads), or the
 // fp32 partial sums of one K split (reduced by splitk_reduce_kernel)
 enum { OUT_BF16 = 0, OUT_F32 = 1, OUT_PART = 2 };
+// fp8 weights already widened to bf16 (exact) in the call's wdq buffer:
+// loaded as bf16, scaled per output channel as fp8 weights are
+constexpr int W_FP8W = 3;
 
 template <int EPI, int WT, int OUT, int BMT>
 __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
@@ -155,7 +158,10 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(1024))) bf16_t smem[STG * (ASTG + W_STAGE)];
   auto sA = [&](int s) { return smem + s * ASTG; };
   auto sW = [&](int s) { return smem + STG * ASTG + s * W_STAGE; };
+  // fp8 weights come as bytes (FP8) or widened to bf16 (W_FP8W, loaded as
+  // bf16); either way the sum is scaled per output channel (SCALED)
   constexpr bool FP8 = WT == W_FP8;
+  constexpr bool SCALED = WT == W_FP8 || WT == W_FP8W;
   // vector-memory instructions per wave per k-tile: A BMT / 64, W 2 (bf16) or 1 (fp8)
   constexpr int VMT = AI + (FP8 ? 1 : 2);
 
@@ -224,7 +230,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
   for (int i = 0; i < FN; ++i) {
     f32x16_t init{};
-    if (!FP8 && !PART && a.bias) {
+    if (!SCALED && !PART && a.bias) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const float4 b = *reinterpret_cast<const float4*>(a.bias + n_base + i * 32 + q * 8 + half * 4);
@@ -368,7 +374,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
       for (int q = 0; q < 4; ++q) {
         const int nl = i * 32 + q * 8 + half * 4;  // column inside the sub-tile
         float4 bias = make_float4(0, 0, 0, 0), scl = make_float4(1, 1, 1, 1);
-        if constexpr (FP8) {
+        if constexpr (SCALED) {
           if (a.bias) bias = *reinterpret_cast<const float4*>(a.bias + n_base + nl);
           scl = *reinterpret_cast<const float4*>(a.scale + n_base + nl);
         }
@@ -377,7 +383,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
           const int ml = j * 32 + frow;
           float v0 = acc[i][j][q * 4 + 0], v1 = acc[i][j][q * 4 + 1];
           float v2 = acc[i][j][q * 4 + 2], v3 = acc[i][j][q * 4 + 3];
-          if constexpr (FP8) {
+          if constexpr (SCALED) {
             v0 = v0 * scl.x + bias.x;
             v1 = v1 * scl.y + bias.y;
             v2 = v2 * scl.z + bias.z;
@@ -1080,53 +1086,116 @@ __global__ __launch_bounds__(256) void widen_fp8_kernel(const uint4* __restrict_
   out[2 * i + 1] = make_uint4(o[4], o[5], o[6], o[7]);
 }
 
+// Launch of kernel K, timed by events e0 (before) and e1 (after) when given.
+template <typename K, typename... Args>
+void launch_ev(K kernel, dim3 grid, dim3 block, hipStream_t st, hipEvent_t e0, hipEvent_t e1, Args... args) {
+  if (e0 || e1)
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, st, e0, e1, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, 0, st, args...);
+}
+
+// The 128- / 256-row MFMA kernel (and the split-K reduction), the product
+// timed by e0 / e1 when given.
 template <int EPI, int WT, bool F32OUT>
-hipError_t launch_mfma(const GemmArgs& a, hipStream_t st) {
-  if constexpr (EPI != EPI_RESID) {
-    if (use_big(a, WT, F32OUT)) {
-      const int tiles = ((a.M + big::BM - 1) / big::BM) * (a.N / big::BN);
-      // a multiple of 8 blocks keeps block b on XCD b % 8 in every round
-      int grid = device_cus() & ~7;
-      grid = grid < 8 ? 8 : grid;
-      grid = tiles < grid ? tiles : grid;
-      if constexpr (WT == W_FP8) {
-        // widen the fp8 weights to bf16 (exact) and scale in the epilogue
-        // (a probe times both launches: start with the widening, stop with
-        // the product)
-        const int64_t n16 = (int64_t)a.N * a.K / 16;
-        const dim3 wgrid((unsigned)((n16 + 255) / 256));
-        const uint4* w8 = reinterpret_cast<const uint4*>(a.W);
-        uint4* w16 = reinterpret_cast<uint4*>(a.wdq);
-        GemmArgs b = a;
-        b.W = a.wdq;
-        if (LaunchProbe* p = launch_probe_take()) {
-          hipExtLaunchKernelGGL(widen_fp8_kernel, wgrid, dim3(256), 0, st, p->start, nullptr, 0, w8, w16, n16);
-          hipExtLaunchKernelGGL((gemm_big_kernel<EPI, true>), dim3(grid), dim3(256), 0, st, nullptr, p->stop, 0, b);
-        } else {
-          hipLaunchKernelGGL(widen_fp8_kernel, wgrid, dim3(256), 0, st, w8, w16, n16);
-          hipLaunchKernelGGL((gemm_big_kernel<EPI, true>), dim3(grid), dim3(256), 0, st, b);
-        }
-      } else {
-        launch_timed(gemm_big_kernel<EPI, false>, dim3(grid), dim3(256), 0, st, a);
-      }
-      return hipGetLastError();
-    }
-  }
+void launch_tiles(const GemmArgs& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   const int bm = gemm_tile_m(a.M, a.N);
   const int tiles = ((a.M + bm - 1) / bm) * (a.N / BN);
   if (a.split > 1) {
     if (bm == 128)
-      launch_timed(gemm_mfma_kernel<EPI, WT, OUT_PART, 128>, dim3(tiles * a.split), dim3(NTHREADS), 0, st, a);
+      launch_ev(gemm_mfma_kernel<EPI, WT, OUT_PART, 128>, dim3(tiles * a.split), dim3(NTHREADS), st, e0, e1, a);
     else
-      launch_timed(gemm_mfma_kernel<EPI, WT, OUT_PART, 256>, dim3(tiles * a.split), dim3(NTHREADS), 0, st, a);
+      launch_ev(gemm_mfma_kernel<EPI, WT, OUT_PART, 256>, dim3(tiles * a.split), dim3(NTHREADS), st, e0, e1, a);
     const int64_t n4 = (int64_t)a.M * (a.N / 4);
-    hipLaunchKernelGGL((splitk_reduce_kernel<EPI, WT == W_FP8, F32OUT>), dim3((unsigned)((n4 + 255) / 256)),
+    hipLaunchKernelGGL((splitk_reduce_kernel<EPI, WT == W_FP8 || WT == W_FP8W, F32OUT>), dim3((unsigned)((n4 + 255) / 256)),
                        dim3(256), 0, st, a);
   } else if (bm == 128) {
-    launch_timed(gemm_mfma_kernel<EPI, WT, F32OUT ? OUT_F32 : OUT_BF16, 128>, dim3(tiles), dim3(NTHREADS), 0, st, a);
+    launch_ev(gemm_mfma_kernel<EPI, WT, F32OUT ? OUT_F32 : OUT_BF16, 128>, dim3(tiles), dim3(NTHREADS), st, e0, e1, a);
   } else {
-    launch_timed(gemm_mfma_kernel<EPI, WT, F32OUT ? OUT_F32 : OUT_BF16, 256>, dim3(tiles), dim3(NTHREADS), 0, st, a);
+    launch_ev(gemm_mfma_kernel<EPI, WT, F32OUT ? OUT_F32 : OUT_BF16, 256>, dim3(tiles), dim3(NTHREADS), st, e0, e1, a);
   }
+}
+
+// Row tiles (of 256) that leave the persistent kernel for the 128-row MFMA
+// kernel.  When the persistent kernel's last round of tiles fills at most half
+// of the grid, that round costs a whole round for a fraction of the work;
+// the rows of its tiles (rounded up to whole row tiles), as 128 x 128 tiles at
+// most two per CU, take about half a round (measured: N = 1,024, K = 4,096: a
+// 256 x 256 round 103 us, a lone 128 x 128 tile 50 us).
+int persistent_peel(int M, int N, int grid) {
+  const int m_tiles = (M + big::BM - 1) / big::BM, num_tn = N / big::BN;
+  const int64_t T = (int64_t)m_tiles * num_tn;
+  const int r = (int)(T % grid);
+  if (r == 0 || 2 * r > grid) return 0;
+  const int p = (r + num_tn - 1) / num_tn;
+  if ((int64_t)(m_tiles - p) * num_tn < 256) return 0;  // the rest must stay persistent
+  const int64_t rows = M - (int64_t)(m_tiles - p) * big::BM;
+  const int64_t small = ((rows + 127) / 128) * (N / BN);
+  return small <= 2 * (int64_t)grid ? p : 0;
+}
+
+template <int EPI, int WT, bool F32OUT>
+hipError_t launch_mfma(const GemmArgs& a, hipStream_t st) {
+  if constexpr (EPI != EPI_RESID) {
+    if (use_big(a, WT, F32OUT)) {
+      // a multiple of 8 blocks keeps block b on XCD b % 8 in every round
+      int grid = device_cus() & ~7;
+      grid = grid < 8 ? 8 : grid;
+      // rows of a last, mostly empty round of tiles go to the 128-row kernel
+      const int peel = persistent_peel(a.M, a.N, grid);
+      GemmArgs b = a;  // the persistent part: the first rows
+      if (peel) b.M = ((a.M + big::BM - 1) / big::BM - peel) * big::BM;
+      const int tiles = ((b.M + big::BM - 1) / big::BM) * (b.N / big::BN);
+      grid = tiles < grid ? tiles : grid;
+      GemmArgs t = a;  // the rest (bf16 activations and output, the caller's weights)
+      t.A = reinterpret_cast<const bf16_t*>(a.A) + (int64_t)b.M * a.lda;
+      t.C = reinterpret_cast<bf16_t*>(a.C) + (int64_t)b.M * a.ldc;
+      t.M = a.M - b.M;
+      t.split = 1;
+      // a probe times every launch of the product: start with the first, stop
+      // with the last
+      LaunchProbe* p = launch_probe_take();
+      hipEvent_t e0 = p ? p->start : nullptr, e1 = p ? p->stop : nullptr;
+      if constexpr (WT == W_FP8) {
+        // widen the fp8 weights to bf16 (exact) and scale in the epilogue
+        const int64_t n16 = (int64_t)a.N * a.K / 16;
+        const dim3 wgrid((unsigned)((n16 + 255) / 256));
+        const uint4* w8 = reinterpret_cast<const uint4*>(a.W);
+        uint4* w16 = reinterpret_cast<uint4*>(a.wdq);
+        b.W = a.wdq;
+        launch_ev(widen_fp8_kernel, wgrid, dim3(256), st, e0, nullptr, w8, w16, n16);
+        launch_ev(gemm_big_kernel<EPI, true>, dim3(grid), dim3(256), st, nullptr, peel ? nullptr : e1, b);
+      } else {
+        launch_ev(gemm_big_kernel<EPI, false>, dim3(grid), dim3(256), st, e0, peel ? nullptr : e1, b);
+      }
+      if (peel) {
+        if constexpr (WT == W_FP8) {
+          t.W = a.wdq;  // widened above
+          launch_tiles<EPI, W_FP8W, F32OUT>(t, st, nullptr, e1);
+        } else {
+          launch_tiles<EPI, WT, F32OUT>(t, st, nullptr, e1);
+        }
+      }
+      return hipGetLastError();
+    }
+  }
+  LaunchProbe* p = launch_probe_take();
+  hipEvent_t e0 = p ? p->start : nullptr, e1 = p ? p->stop : nullptr;
+  if constexpr (WT == W_FP8) {
+    if (a.wdq) {
+      // with a widening buffer: the weights widened to bf16 once, then the
+      // bf16 loads (converting fp8 fragments inside the k-loop is about 4x
+      // slower: M = 981, N = 5,120, K = 1,280: 117 against 25 us)
+      const int64_t n16 = (int64_t)a.N * a.K / 16;
+      launch_ev(widen_fp8_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), st, e0, nullptr,
+                reinterpret_cast<const uint4*>(a.W), reinterpret_cast<uint4*>(a.wdq), n16);
+      GemmArgs b = a;
+      b.W = a.wdq;
+      launch_tiles<EPI, W_FP8W, F32OUT>(b, st, nullptr, e1);
+      return hipGetLastError();
+    }
+  }
+  launch_tiles<EPI, WT, F32OUT>(a, st, e0, e1);
   return hipGetLastError();
 }
 

@@ -165,7 +165,9 @@ def test_gemm_bf16_epilogues(M, N, K, cuda):
 
 # Large-M shapes of the persistent 256 x 256 kernel (store and gelu epilogues):
 # several tiles per block, a ragged last m-tile, K of 2 and 16 k-tiles of 64.
-PERSISTENT_SHAPES = [(20000, 1024, 1024), (53205 // 4, 3072, 128), (9000, 4096, 256)]
+# The first three leave a last round of tiles at most half full on 256 CUs,
+# whose rows then run on the 128-row kernel; the fourth fills whole rounds.
+PERSISTENT_SHAPES = [(20000, 1024, 1024), (53205 // 4, 3072, 128), (9000, 4096, 256), (16380, 1024, 512)]
 
 
 @pytest.mark.parametrize("M,N,K", PERSISTENT_SHAPES)
@@ -295,6 +297,20 @@ def test_gemm_fp8_weights(M, N, K, cuda):
     R = R0.clone()
     _gemm(A, qd, b, capi.EPI_RESID, capi.WT_FP8, R=R, scale=sd)
     assert ((R - (R0 + acc)).abs() <= acc.abs() * 2 ** -8 + 1e-4).all()
+    # with a widening buffer the weights are widened to bf16 first (exactly);
+    # below the persistent kernel's size the same products are summed in the
+    # same order: the same bits
+    wdq = torch.empty(N, K, dtype=torch.bfloat16, device=cuda)
+    same = -(-M // 256) * (N // 256) < 256
+    Cw = _gemm(A, qd, b, capi.EPI_STORE, capi.WT_FP8, scale=sd, wdq=wdq).float()
+    assert torch.equal(Cw, C_) if same else ((Cw - acc).abs() <= acc.abs() * 2 ** -8 + 1e-4).all()
+    Rw = R0.clone()
+    _gemm(A, qd, b, capi.EPI_RESID, capi.WT_FP8, R=Rw, scale=sd, wdq=wdq)
+    assert torch.equal(Rw, R)
+    if same:
+        Cg = _gemm(A, qd, b, capi.EPI_GELU, capi.WT_FP8, scale=sd).float()
+        Cgw = _gemm(A, qd, b, capi.EPI_GELU, capi.WT_FP8, scale=sd, wdq=wdq).float()
+        assert torch.equal(Cgw, Cg)
 
 
 @pytest.mark.parametrize("M,N,K", PERSISTENT_SHAPES)
