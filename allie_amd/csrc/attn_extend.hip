@@ -367,11 +367,13 @@ ALLIE_DEV uint32_t pk_f16(float a, float b) { return __builtin_bit_cast(uint32_t
 // r at j ^ (4 ((r >> 1) & 1)), read transposed), DEPTH chunks loading into
 // registers while one is multiplied.  First the
 // group's prefix (query i sees positions below min(P, pos[i])), then the
-// tile's private keys as columns: for each extra index e, a run of
-// consecutive tokens whose e-th private key is the same pool slot (siblings'
-// common ancestors) is one column, visible to exactly that run of queries.
-// Every (token, e) entry lands in exactly one column, so each query sees each
-// of its private keys once, whatever the slots are.
+// tile's private keys other than the tokens' own as columns: for each extra
+// index e, a run of consecutive tokens whose e-th private key is the same
+// pool slot (siblings' common ancestors) is one column, visible to exactly
+// that run of queries.  Every (token, e) entry lands in exactly one column,
+// so each query sees each of those keys once, whatever the slots are.  A
+// token's own key and value (its last private key, written to the cache from
+// its qkv row before attention) are read from that row and open its softmax.
 constexpr int TREE_EB = 8;  // extra indices per column batch
 // K rows (bf16, 128 B): 16-byte chunk c of row r at c ^ kswz(r)
 ALLIE_DEV int kswz(int r) { return (r >> 1) & 7; }
@@ -437,7 +439,8 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
 #pragma unroll
       for (int e = 0; e < TREE_EB; ++e) {
         const int ee = eb + e;
-        const int v = (ee < E) ? a.extra_slot[(int64_t)i * a.max_extra + ee] : -1;
+        // the last private key is the token's own: it is taken from its qkv row
+        const int v = (ee < E - 1) ? a.extra_slot[(int64_t)i * a.max_extra + ee] : -1;
         sl[e] = (v >= 0 && (v >> 4) < a.pool_blocks) ? v : -1;
       }
 #pragma unroll
@@ -483,6 +486,40 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
   const float c2 = a.scale * 1.4426950408889634f;
   float m_run = -INFINITY, l_run = 0.f;
   f32x4_t o[4] = {f32x4_t{}, f32x4_t{}, f32x4_t{}, f32x4_t{}};  // O^T: dims 16 db + 4 lg .. +3 of query lq
+  {
+    // The token's own key and value (its last private key, which the cache
+    // holds as a copy of them) come from its qkv row: the softmax starts from
+    // that key, and the columns carry only the other private keys (a tree
+    // level's own keys would otherwise be one column per query).
+    const int E = q_ok ? a.n_extra[qi] : 0;
+    const bool has_self = E >= 1;
+    const bf16_t* row = qkv + (int64_t)qi * ld + head * HD;
+    float sdot = 0.f;
+    uint2 vs[4] = {};
+    if (has_self) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const u32x4_t kw = *reinterpret_cast<const u32x4_t*>(row + d + 32 * ks + 8 * lg);
+        const u32x4_t qw = __builtin_bit_cast(u32x4_t, qf[ks]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sdot = fmaf(bf2f(qw[e] & 0xffffu), bf2f(kw[e] & 0xffffu), sdot);
+          sdot = fmaf(bf2f(qw[e] >> 16), bf2f(kw[e] >> 16), sdot);
+        }
+      }
+#pragma unroll
+      for (int db = 0; db < 4; ++db) vs[db] = *reinterpret_cast<const uint2*>(row + 2 * d + 16 * db + 4 * lg);
+    }
+    sdot += __shfl_xor(sdot, 16, 64);  // the query's four lane groups hold 16 dims each
+    sdot += __shfl_xor(sdot, 32, 64);
+    if (has_self) {
+      m_run = sdot;
+      l_run = lg == 0 ? 1.f : 0.f;  // the row sum is split over the lane groups
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+        o[db] = f32x4_t{bf2f(vs[db].x & 0xffffu), bf2f(vs[db].x >> 16), bf2f(vs[db].y & 0xffffu), bf2f(vs[db].y >> 16)};
+    }
+  }
   const bool wave_busy = wave * 16 < ntok;  // a wave past the tile's tokens only stages keys
   const int trow = lq >> 2, tchunk = lq & 3;  // transposing read: key row within 4, 4-dim chunk
   const int nchp = (P + KT - 1) / KT;
