@@ -372,8 +372,8 @@ ALLIE_DEV uint32_t pk_f16(float a, float b) { return __builtin_bit_cast(uint32_t
 // pool slot (siblings' common ancestors) is one column, visible to exactly
 // that run of queries.  Every (token, e) entry lands in exactly one column,
 // so each query sees each of those keys once, whatever the slots are.  A
-// token's own key and value (its last private key, written to the cache from
-// its qkv row before attention) are read from that row and open its softmax.
+// token's own key and value (its last private key) are read by the token's
+// own lanes from its slot and open its softmax.
 constexpr int TREE_EB = 8;  // extra indices per column batch
 // K rows (bf16, 128 B): 16-byte chunk c of row r at c ^ kswz(r)
 ALLIE_DEV int kswz(int r) { return (r >> 1) & 7; }
@@ -487,19 +487,24 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
   float m_run = -INFINITY, l_run = 0.f;
   f32x4_t o[4] = {f32x4_t{}, f32x4_t{}, f32x4_t{}, f32x4_t{}};  // O^T: dims 16 db + 4 lg .. +3 of query lq
   {
-    // The token's own key and value (its last private key, which the cache
-    // holds as a copy of them) come from its qkv row: the softmax starts from
-    // that key, and the columns carry only the other private keys (a tree
-    // level's own keys would otherwise be one column per query).
+    // The token's own key and value (its last private key) are read from its
+    // slot by its own lanes: the softmax starts from that key, and the
+    // columns carry only the other private keys (a tree level's own keys
+    // would otherwise be one column per query).
     const int E = q_ok ? a.n_extra[qi] : 0;
-    const bool has_self = E >= 1;
-    const bf16_t* row = qkv + (int64_t)qi * ld + head * HD;
+    int sl = -1;
+    if (E >= 1 && E <= a.max_extra) {
+      const int v = a.extra_slot[(int64_t)qi * a.max_extra + E - 1];
+      sl = (v >= 0 && (v >> 4) < a.pool_blocks) ? v : -1;
+    }
+    const bool has_self = sl >= 0;
+    const bf16_t* row = lbase + (int64_t)(has_self ? sl >> 4 : 0) * bstride + (sl & 15) * HD;
     float sdot = 0.f;
     uint2 vs[4] = {};
     if (has_self) {
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const u32x4_t kw = *reinterpret_cast<const u32x4_t*>(row + d + 32 * ks + 8 * lg);
+        const u32x4_t kw = *reinterpret_cast<const u32x4_t*>(row + 32 * ks + 8 * lg);
         const u32x4_t qw = __builtin_bit_cast(u32x4_t, qf[ks]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -508,7 +513,7 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
         }
       }
 #pragma unroll
-      for (int db = 0; db < 4; ++db) vs[db] = *reinterpret_cast<const uint2*>(row + 2 * d + 16 * db + 4 * lg);
+      for (int db = 0; db < 4; ++db) vs[db] = *reinterpret_cast<const uint2*>(row + voff + 16 * db + 4 * lg);
     }
     sdot += __shfl_xor(sdot, 16, 64);  // the query's four lane groups hold 16 dims each
     sdot += __shfl_xor(sdot, 32, 64);

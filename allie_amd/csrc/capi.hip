@@ -289,8 +289,17 @@ PrefillWS layout_prefill(const allie_model* m, int B, int T, char* base) {
 
 // part: workspace of the K-split partial sums (part_bytes), or null
 // wdq: [4 d^2] bf16 workspace for fp8 weights on the persistent kernel, or null
+// Keys and values of an extend's QKV projection written straight to the KV
+// pool (layer `layer`, row m at slot[m]) by the GEMM when it can
+struct KVDest {
+  void* pool;
+  const int32_t* slot;
+  int layer, pool_blocks;
+};
+
 int gemm(const allie_model* m, const void* A, const void* W, const float* bias, const float* scale,
-         void* C, float* R, int M, int N, int K, int epi, int probe_kind, float* part, void* wdq, hipStream_t st) {
+         void* C, float* R, int M, int N, int K, int epi, int probe_kind, float* part, void* wdq, hipStream_t st,
+         const KVDest* kv = nullptr, bool* kv_done = nullptr) {
   GemmArgs g{};
   g.A = A;
   g.W = W;
@@ -310,6 +319,14 @@ int gemm(const allie_model* m, const void* A, const void* W, const float* bias, 
   g.split = (part && g.wtype != W_F32) ? gemm_split_factor(M, N, K) : 1;
   g.part = part;
   g.wdq = g.wtype == W_FP8 ? wdq : nullptr;
+  if (kv) {
+    g.kv_pool = kv->pool;
+    g.kv_slot = kv->slot;
+    g.kv_layer = kv->layer;
+    g.kv_pool_blocks = kv->pool_blocks;
+    if (!gemm_stores_kv(g)) g.kv_pool = nullptr, g.kv_slot = nullptr;
+  }
+  if (kv_done) *kv_done = g.kv_pool != nullptr;
   HIP_TRY(probe_mark(probe_kind, true, st));
   hipError_t e = launch_gemm(g, st);
   if (e != hipSuccess) return fail(ALLIE_ERR_HIP, "gemm M=%d N=%d K=%d: %s", M, N, K, hipGetErrorString(e));
@@ -362,8 +379,11 @@ struct Compact {
 
 // The transformer blocks over T rows whose embeddings (h) and first ln_1 (x)
 // are in place.  kv_slot/kv_pool: every layer's keys and values of row t are
-// written to pool slot kv_slot[t] (before attention runs).  attn(layer) runs
-// the attention of one layer from acts.qkv into acts.attn.
+// written to pool slot kv_slot[t] (before attention runs); with kv_only_pool
+// the QKV GEMM may write them there instead of into acts.qkv (whose key and
+// value columns are then left unwritten: the attention reads them from the
+// pool).  attn(layer) runs the attention of one layer from acts.qkv into
+// acts.attn.
 //
 // The attention and MLP output projections end in the residual add
 // h += bf16(y + b) (src/modeling/model.py:50-55 -> [lib] GPT2Block).  Small-M
@@ -375,8 +395,8 @@ struct Compact {
 // null.
 template <typename AttnFn>
 int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slot, void* kv_pool,
-               int kv_pool_blocks, AttnFn&& attn, hipStream_t st, const Compact* cp, const float** h_final,
-               const void** final_add) {
+               int kv_pool_blocks, bool kv_only_pool, AttnFn&& attn, hipStream_t st, const Compact* cp,
+               const float** h_final, const void** final_add) {
   const int d = m->d, L = m->L, act = m->act_bf16;
   *final_add = nullptr;
   *h_final = w.h;
@@ -424,8 +444,12 @@ int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slo
   };
   for (int li = 0; li < L; ++li) {
     const LayerW& l = m->layers[li];
-    if ((rc = gemm(m, w.x, l.w_qkv, l.b_qkv, l.s_qkv, w.qkv, nullptr, T, 3 * d, d, EPI_STORE, ALLIE_PROBE_QKV, w.part, w.wdq, st))) return rc;
-    if (kv_pool && kv_slot) {
+    const KVDest kvd{kv_pool, kv_slot, li, kv_pool_blocks};
+    bool kv_done = false;
+    if ((rc = gemm(m, w.x, l.w_qkv, l.b_qkv, l.s_qkv, w.qkv, nullptr, T, 3 * d, d, EPI_STORE, ALLIE_PROBE_QKV, w.part,
+                   w.wdq, st, (kv_only_pool && kv_pool && kv_slot) ? &kvd : nullptr, &kv_done)))
+      return rc;
+    if (kv_pool && kv_slot && !kv_done) {
       KVWriteArgs kw{};
       kw.qkv = w.qkv;
       kw.slot = kv_slot;
@@ -906,7 +930,7 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
   }
   const void* final_add = nullptr;
   const float* h_final = nullptr;
-  rc = run_layers(m, acts, (int)T, kv_pool ? w.slot : nullptr, kv_pool, kv_pool_blocks,
+  rc = run_layers(m, acts, (int)T, kv_pool ? w.slot : nullptr, kv_pool, kv_pool_blocks, false,
                   [&](int layer) -> int {
                     HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, true, st));
                     aa.order_ready = layer > 0;  // the game order is computed once per forward
@@ -1070,7 +1094,7 @@ int extend_run(allie_model* m, const ExtendPlan& plan, const ExtendWS& w, const 
   const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff, w.part, w.wdq};
   const void* final_add = nullptr;
   const float* h_final = nullptr;
-  rc = run_layers(m, acts, n_tok, w.self_slot, kv_pool, kv_pool_blocks,
+  rc = run_layers(m, acts, n_tok, w.self_slot, kv_pool, kv_pool_blocks, true,
                   [&](int layer) -> int {
                     xa.layer = layer;
                     if (tree) {

@@ -442,6 +442,23 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
           r[1] = x1;
         }
       }
+    } else if (EPI == EPI_STORE && a.kv_pool && n_base >= a.N / 3) {
+      // an extend's keys and values: this wave's 64 columns are one head's
+      // key or value; row m goes to its pool slot (16 positions per block)
+      const int d = a.N / 3, H = d / 64;
+      const int kvi = n_base >= 2 * d ? 1 : 0, head = (n_base - (kvi + 1) * d) / 64;
+      bf16_t* pl = reinterpret_cast<bf16_t*>(a.kv_pool) + ((int64_t)a.kv_layer * a.kv_pool_blocks * 2 + kvi) * H * 1024 +
+                   (int64_t)head * 1024 + cl;
+#pragma unroll 4
+      for (int it = 0; it < WMX / 8; ++it) {
+        const int ml = it * 8 + (lane >> 3);
+        const int m = m0 + wm * WMX + ml;
+        const uint4 v = *reinterpret_cast<const uint4*>(reg + ml * EP + cl);
+        if (m >= a.M) continue;
+        const int sl = a.kv_slot[m];
+        if (sl < 0 || (sl >> 4) >= a.kv_pool_blocks) continue;
+        *reinterpret_cast<uint4*>(pl + ((int64_t)(sl >> 4) * 2 * H * 16 + (sl & 15)) * 64) = v;
+      }
     } else {
 #pragma unroll 4
       for (int it = 0; it < WMX / 8; ++it) {
@@ -596,7 +613,7 @@ ALLIE_DEV float acc_read(float v) {
 // SCALED: weights that were fp8 (widened exactly to bf16 for this call) with
 // a per-output-channel scale: the accumulators start at 0 and the epilogue
 // takes acc * scale + bias (the 256x128 kernel's order for fp8 weights).
-template <int EPI, bool SCALED>
+template <int EPI, bool SCALED, bool KV>
 __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
 #if defined(__HIP_DEVICE_COMPILE__)
   // the 256 x 256 geometry (shadows the 256 x 128 kernel's constants)
@@ -834,6 +851,24 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
     for (; kt + 2 < KT; ++kt) k_tile(cur, kt, DMA, std::true_type{});
     for (; kt < KT; ++kt) k_tile(cur, kt, 0, std::false_type{});
 
+    // KV: a tile of key / value columns goes to the pool, row by row at the
+    // rows' slots; the slots of this lane's 16 rows load before the next
+    // tile's head, so waiting for them does not wait for that
+    const int d3 = a.N / 3;
+    const bool kv_tile = KV && cur.n0 + big::BN > d3;
+    int slot[FM][4];
+    if constexpr (KV) {
+      if (kv_tile) {
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+#pragma unroll
+          for (int it = 0; it < 4; ++it) {
+            const int m = cur.m0 + wm * 128 + j * 32 + it * 8 + rl;
+            slot[j][it] = m < a.M ? a.kv_slot[m] : -1;
+          }
+      }
+    }
+
     // the next tile's head loads while this one is written out
     const int t_next = t + gridDim.x;
     const bool more = t_next < tiles;
@@ -847,6 +882,14 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
     const auto rC = rsrc_C(cur);
     const int ldc2 = opaque_s(a.ldc * 2);
     const uint32_t c_lane = (uint32_t)((wm * 128 + rl) * ldc2 + (cur.n0 + n_wave + cl) * 2);
+    // KV: the layer's slice of the pool; a 64-column chunk is one head's key
+    // or value, row m at ((block 2 + kv) H + head) 16 + offset of its slot
+    const int Hh = d3 / 64;
+    const uint32_t pool_bytes = (uint32_t)a.kv_pool_blocks * 2u * (uint32_t)Hh * 2048u;
+    const auto rP = __builtin_amdgcn_make_buffer_rsrc(
+        KV ? reinterpret_cast<bf16_t*>(a.kv_pool) + (int64_t)a.kv_layer * a.kv_pool_blocks * 2 * Hh * 1024
+           : reinterpret_cast<bf16_t*>(a.C),
+        (short)0, KV ? (int)pool_bytes : 0, 0x00020000);
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
 #pragma unroll
@@ -886,14 +929,27 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
         u32x4_t v[4];
         lds_read_b128x4(reg + rl * EP + cl, reg + (8 + rl) * EP + cl, reg + (16 + rl) * EP + cl,
                         reg + (24 + rl) * EP + cl, v);
+        const int c0 = cur.n0 + n_wave + h * 64;  // 64-aligned: q, or one head's key or value
+        if (KV && kv_tile && c0 >= d3) {
+          const int kvi = c0 >= 2 * d3 ? 1 : 0, head = (c0 - (kvi + 1) * d3) >> 6;
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
-          // row wm 128 + j 32 + it 8 + rl, column n0 + n_wave + h 64 + cl; a
-          // non-temporal store (cache policy nt): the output is not read
-          // again by this kernel, and kept out of L2 it leaves the A and W
-          // panels there (QKV 7%, fc 3% faster)
-          __builtin_amdgcn_raw_buffer_store_b128(v[it], rC, c_lane + (uint32_t)((j * 32 + it * 8) * ldc2 + h * 128),
-                                                 0, 2);
+          for (int it = 0; it < 4; ++it) {
+            const int sl = slot[j][it];
+            const bool ok = sl >= 0 && (sl >> 4) < a.kv_pool_blocks;
+            const uint32_t off = ok ? ((((uint32_t)(sl >> 4) * 2u + kvi) * Hh + head) * 16u + (sl & 15)) * 128u + cl * 2
+                                    : 0xffffffffu;  // outside the buffer: dropped
+            __builtin_amdgcn_raw_buffer_store_b128(v[it], rP, off, 0, 2);
+          }
+        } else {
+#pragma unroll
+          for (int it = 0; it < 4; ++it) {
+            // row wm 128 + j 32 + it 8 + rl, column n0 + n_wave + h 64 + cl; a
+            // non-temporal store (cache policy nt): the output is not read
+            // again by this kernel, and kept out of L2 it leaves the A and W
+            // panels there (QKV 7%, fc 3% faster)
+            __builtin_amdgcn_raw_buffer_store_b128(v[it], rC, c_lane + (uint32_t)((j * 32 + it * 8) * ldc2 + h * 128),
+                                                   0, 2);
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -1152,6 +1208,7 @@ hipError_t launch_mfma(const GemmArgs& a, hipStream_t st) {
       t.C = reinterpret_cast<bf16_t*>(a.C) + (int64_t)b.M * a.ldc;
       t.M = a.M - b.M;
       t.split = 1;
+      if (a.kv_slot) t.kv_slot = a.kv_slot + b.M;
       // a probe times every launch of the product: start with the first, stop
       // with the last
       LaunchProbe* p = launch_probe_take();
@@ -1164,9 +1221,15 @@ hipError_t launch_mfma(const GemmArgs& a, hipStream_t st) {
         uint4* w16 = reinterpret_cast<uint4*>(a.wdq);
         b.W = a.wdq;
         launch_ev(widen_fp8_kernel, wgrid, dim3(256), st, e0, nullptr, w8, w16, n16);
-        launch_ev(gemm_big_kernel<EPI, true>, dim3(grid), dim3(256), st, nullptr, peel ? nullptr : e1, b);
+        if (EPI == EPI_STORE && a.kv_pool)
+          launch_ev(gemm_big_kernel<EPI_STORE, true, true>, dim3(grid), dim3(256), st, nullptr, peel ? nullptr : e1, b);
+        else
+          launch_ev(gemm_big_kernel<EPI, true, false>, dim3(grid), dim3(256), st, nullptr, peel ? nullptr : e1, b);
       } else {
-        launch_ev(gemm_big_kernel<EPI, false>, dim3(grid), dim3(256), st, e0, peel ? nullptr : e1, b);
+        if (EPI == EPI_STORE && a.kv_pool)
+          launch_ev(gemm_big_kernel<EPI_STORE, false, true>, dim3(grid), dim3(256), st, e0, peel ? nullptr : e1, b);
+        else
+          launch_ev(gemm_big_kernel<EPI, false, false>, dim3(grid), dim3(256), st, e0, peel ? nullptr : e1, b);
       }
       if (peel) {
         if constexpr (WT == W_FP8) {
@@ -1207,6 +1270,14 @@ bool gemm_uses_persistent(const GemmArgs& a) {
   return a.M > 0 && (a.epi == EPI_STORE || a.epi == EPI_GELU) && use_big(a, a.wtype, a.out_f32 != 0);
 }
 
+bool gemm_stores_kv(const GemmArgs& a) {
+  if (!a.kv_pool || !a.kv_slot || a.M <= 0 || a.epi != EPI_STORE || a.out_f32 || a.wtype == W_F32) return false;
+  if (a.N % 192 != 0 || a.ldc != a.N || a.split > 1 || gemm_skinny_supported(a) || !gemm_mfma_supported(a))
+    return false;
+  // the persistent kernel addresses one layer's slice with 32-bit offsets
+  return (int64_t)a.kv_pool_blocks * 2 * (a.N / 192) * 2048 < ((int64_t)1 << 31);
+}
+
 bool gemm_mfma_supported(const GemmArgs& a) {
   return a.N % BN == 0 && a.K % BK == 0 && a.lda % 8 == 0 && a.M > 0;
 }
@@ -1238,6 +1309,7 @@ int gemm_split_factor(int M, int N, int K) {
 
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t st) {
   if (a.M == 0) return hipSuccess;
+  if (a.kv_pool && !gemm_stores_kv(a)) return hipErrorInvalidValue;
   if (a.wtype != W_F32 && gemm_skinny_supported(a)) return launch_gemm_skinny(a, st);
   if (a.wtype == W_F32) {
     dim3 grid((a.N + 63) / 64, (a.M + 63) / 64);
@@ -1251,6 +1323,7 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t st) {
   }
   if (!gemm_mfma_supported(a)) return hipErrorInvalidValue;
   if (a.split > 1 && (a.part == nullptr || (a.K / BK) % a.split != 0)) return hipErrorInvalidValue;
+  if (a.kv_pool && !gemm_stores_kv(a)) return hipErrorInvalidValue;
   if (a.wtype == W_BF16) {
     switch (a.epi) {
       case EPI_STORE:

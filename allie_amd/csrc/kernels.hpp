@@ -109,6 +109,13 @@ struct GemmArgs {
   float* part;         // [split][M][N] fp32 partial sums when split > 1
   void* wdq;           // W_FP8: [N][K] bf16 buffer the weights are widened into for the
                        // persistent kernel (large M), or null
+  // An extend's QKV projection (EPI_STORE, N = 3 d): with kv_pool set the key
+  // and value columns [d, 3 d) of row m go to pool slot kv_slot[m] of layer
+  // kv_layer ([layer][kv_pool_blocks][k|v][head][16][64] bf16) instead of C;
+  // rows with a slot outside the pool are not written (see gemm_stores_kv)
+  void* kv_pool;
+  const int32_t* kv_slot;
+  int kv_layer, kv_pool_blocks;
 };
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t st);
 bool gemm_mfma_supported(const GemmArgs& a);
@@ -122,6 +129,9 @@ hipError_t launch_gemm_skinny(const GemmArgs& a, hipStream_t st);
 // and MLP projections with a store epilogue and adds them to the residual
 // stream in the following LayerNorm
 bool gemm_uses_persistent(const GemmArgs& a);
+// true when launch_gemm writes this QKV GEMM's keys and values to a.kv_pool
+// itself (MFMA kernels with bf16 output); otherwise the caller copies them
+bool gemm_stores_kv(const GemmArgs& a);
 // block rows of the 256x128-class kernel for an M x N output: 256, or 128
 // when 256-row tiles would not cover a 256-CU device
 int gemm_tile_m(int M, int N);
