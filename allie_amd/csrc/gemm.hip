@@ -906,11 +906,11 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
     // KV: the layer's slice of the pool; a 64-column chunk is one head's key
     // or value, row m at ((block 2 + kv) H + head) 16 + offset of its slot
     const int Hh = d3 / 64;
-    const uint32_t pool_bytes = (uint32_t)a.kv_pool_blocks * 2u * (uint32_t)Hh * 2048u;
+    const uint32_t pool_bytes = (uint32_t)a.kv_pool_blocks * 2u * (uint32_t)Hh * 2048u;  // < 4 GiB (host check)
     const auto rP = __builtin_amdgcn_make_buffer_rsrc(
         KV ? reinterpret_cast<bf16_t*>(a.kv_pool) + (int64_t)a.kv_layer * a.kv_pool_blocks * 2 * Hh * 1024
            : reinterpret_cast<bf16_t*>(a.C),
-        (short)0, KV ? (int)pool_bytes : 0, 0x00020000);
+        (short)0, KV ? __builtin_bit_cast(int, pool_bytes) : 0, 0x00020000);
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
 #pragma unroll
@@ -1296,7 +1296,8 @@ bool gemm_stores_kv(const GemmArgs& a) {
   if (a.N % 192 != 0 || a.ldc != a.N || a.split > 1 || gemm_skinny_supported(a) || !gemm_mfma_supported(a))
     return false;
   // the persistent kernel addresses one layer's slice with 32-bit offsets
-  return (int64_t)a.kv_pool_blocks * 2 * (a.N / 192) * 2048 < ((int64_t)1 << 31);
+  const bool big = use_big(a, a.wtype, a.out_f32 != 0);
+  return !big || (int64_t)a.kv_pool_blocks * 2 * (a.N / 192) * 2048 < ((int64_t)1 << 32);
 }
 
 bool gemm_mfma_supported(const GemmArgs& a) {
