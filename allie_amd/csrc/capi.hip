@@ -414,16 +414,23 @@ int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slo
     ln.eps = m->cfg.eps;
     ln.y = x;
     ln.act_bf16 = act;
+    // With both projections stored as bf16 and a next layer, the attention
+    // projection's y goes to the qkv buffer (free once attention has read it)
+    // and reaches h only in the next ln_1, with the MLP's: ln_2 normalises
+    // h + y_attn without writing h back (8 instead of 12 bytes per element),
+    // and ln_1 writes (h + y_attn) + y_mlp, the reference's order of the adds.
+    const bool defer = fuse_proj && fuse_fc2 && li + 1 < L && x == w.x;
+    void* y_attn = defer ? w.qkv : x;
     int r;
     if (fuse_proj) {
-      if ((r = gemm(m, attn_in, l.w_o, l.b_o, l.s_o, x, nullptr, M, d, d, EPI_STORE, ALLIE_PROBE_PROJ, w.part, w.wdq, st))) return r;
+      if ((r = gemm(m, attn_in, l.w_o, l.b_o, l.s_o, y_attn, nullptr, M, d, d, EPI_STORE, ALLIE_PROBE_PROJ, w.part, w.wdq, st))) return r;
     } else {
       if ((r = gemm(m, attn_in, l.w_o, l.b_o, l.s_o, nullptr, h, M, d, d, EPI_RESID, ALLIE_PROBE_PROJ, w.part, w.wdq, st))) return r;
     }
     ln.g = l.ln2_g;
     ln.b = l.ln2_b;
-    ln.add = fuse_proj ? x : nullptr;
-    ln.h_out = fuse_proj ? h : nullptr;
+    ln.add = fuse_proj ? y_attn : nullptr;
+    ln.h_out = (fuse_proj && !defer) ? h : nullptr;
     HIP_TRY(launch_layernorm(ln, st));
     if ((r = gemm(m, x, l.w_fc, l.b_fc, l.s_fc, ff, nullptr, M, 4 * d, d, EPI_GELU, ALLIE_PROBE_FC, w.part, w.wdq, st))) return r;
     if (fuse_fc2) {
@@ -434,7 +441,8 @@ int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slo
     if (li + 1 < L) {
       ln.g = m->layers[li + 1].ln1_g;
       ln.b = m->layers[li + 1].ln1_b;
-      ln.add = fuse_fc2 ? x : nullptr;
+      ln.add = fuse_fc2 ? (defer ? y_attn : x) : nullptr;
+      ln.add2 = defer ? x : nullptr;
       ln.h_out = fuse_fc2 ? h : nullptr;
       HIP_TRY(launch_layernorm(ln, st));
     } else {

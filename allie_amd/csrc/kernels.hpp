@@ -82,6 +82,9 @@ struct LNArgs {
   // h_out is set (may alias h)
   const void* add;
   float* h_out;
+  // optional second addend (bf16 [rows][d], with add set): the row is
+  // (h + add) + add2, summed in that order
+  const void* add2;
 };
 hipError_t launch_layernorm(const LNArgs& a, hipStream_t st);
 

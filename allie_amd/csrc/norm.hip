@@ -138,6 +138,13 @@ __global__ __launch_bounds__(256) void layernorm_kernel(allie::LNArgs a) {
       v[i].y += bf2f(y.x >> 16);
       v[i].z += bf2f(y.y & 0xffffu);
       v[i].w += bf2f(y.y >> 16);
+      if (a.add2) {
+        const uint2 z = *reinterpret_cast<const uint2*>(reinterpret_cast<const bf16_t*>(a.add2) + src * d + c);
+        v[i].x += bf2f(z.x & 0xffffu);
+        v[i].y += bf2f(z.x >> 16);
+        v[i].z += bf2f(z.y & 0xffffu);
+        v[i].w += bf2f(z.y >> 16);
+      }
     }
   }
   if (a.h_out) {
@@ -217,7 +224,7 @@ hipError_t launch_embed_ln(const EmbedArgs& a, hipStream_t st) {
 
 hipError_t launch_layernorm(const LNArgs& a, hipStream_t st) {
   if (a.d % 256 != 0 || a.rows_out < a.rows) return hipErrorInvalidValue;
-  if (a.add && !a.act_bf16) return hipErrorInvalidValue;
+  if ((a.add && !a.act_bf16) || (a.add2 && !a.add)) return hipErrorInvalidValue;
   if (a.rows_out == 0) return hipSuccess;
   dim3 grid((a.rows_out + 3) / 4);
   ALLIE_NV_SWITCH(a.d / 256, hipLaunchKernelGGL(layernorm_kernel<NV>, grid, dim3(256), 0, st, a));
