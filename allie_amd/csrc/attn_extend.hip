@@ -316,17 +316,36 @@ __global__ __launch_bounds__(256) void attn_extend_wave_kernel(ExtendAttnArgs a)
     fetch16<T>(pool + off, kr);
     fetch16<T>(pool + off + voff, vr);
   };
+  // private keys that fit one chunk (a decode step's own key) are requested
+  // first, with no dependent round trip after the prefix's last chunk, and
+  // reduced last; only the lanes of real keys load
+  const bool x1 = E > 0 && E <= KV_BLOCK;
+  Row16<T> kX, vX;
+  bool okX = false;
+  if (x1) {
+    int64_t off;
+    locate(nbp, off, okX);
+    if (okX) {
+      fetch16<T>(pool + off, kX);
+      fetch16<T>(pool + off + voff, vX);
+    } else {
+#pragma unroll
+      for (int j = 0; j < (int)sizeof(T); ++j) kX.v[j] = vX.v[j] = make_uint4(0, 0, 0, 0);
+    }
+  }
+  const int nloop = x1 ? nbp : nch;
   // two register buffers: chunk c + 1 loads while chunk c is reduced
   Row16<T> kA, vA, kB, vB;
   bool okA = false, okB = false;
-  if (nch > 0) fetch_chunk(0, kA, vA, okA);
-  for (int c = 0; c < nch; c += 2) {
-    if (c + 1 < nch) fetch_chunk(c + 1, kB, vB, okB);
+  if (nloop > 0) fetch_chunk(0, kA, vA, okA);
+  for (int c = 0; c < nloop; c += 2) {
+    if (c + 1 < nloop) fetch_chunk(c + 1, kB, vB, okB);
     reduce_chunk(kA, vA, okA);
-    if (c + 1 >= nch) break;
-    if (c + 2 < nch) fetch_chunk(c + 2, kA, vA, okA);
+    if (c + 1 >= nloop) break;
+    if (c + 2 < nloop) fetch_chunk(c + 2, kA, vA, okA);
     reduce_chunk(kB, vB, okB);
   }
+  if (x1) reduce_chunk(kX, vX, okX);
   // combine the 16 key lanes of each head-dim group
 #pragma unroll
   for (int o = 4; o < 64; o <<= 1) {
