@@ -206,8 +206,10 @@ ALLIE_DEV float dpp_f(float x) {
 }
 ALLIE_DEV float readlane_f(float x, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)); }
 
+// bf16: held to 128 registers, four waves per SIMD (the fp32 check mode
+// would spill there)
 template <typename T>
-__global__ __launch_bounds__(256) void attn_extend_wave_kernel(ExtendAttnArgs a) {
+__global__ __launch_bounds__(256, sizeof(T) == 2 ? 4 : 1) void attn_extend_wave_kernel(ExtendAttnArgs a) {
   const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int H = a.n_head, d = H * HD;
   if (wid >= (int64_t)a.n * H) return;  // no barriers below: whole waves leave
@@ -249,21 +251,28 @@ __global__ __launch_bounds__(256) void attn_extend_wave_kernel(ExtendAttnArgs a)
   const int nch = nbp + (E + KV_BLOCK - 1) / KV_BLOCK;
   const int32_t* btab = a.prefix_blocks + (int64_t)g * a.max_blocks;
   const int my_blk = lane < nbp ? btab[lane] : -1;  // the first 64 blocks of the row
+  // key kj of chunk c: offset of its key row, visible or not.  A key that is
+  // not visible still reads a written row, one whose product with p = 0 is
+  // zero (unwritten pool memory may hold NaN patterns): past the prefix the
+  // block's first position, past the private keys the token's own slot
+  // (written by this layer's QKV projection).  A block outside the pool
+  // (a batch the prepare step flags) reads block 0.
   auto locate = [&](int c, int64_t& off, bool& ok) {
     int blk, kpos;
     if (c < nbp) {
       blk = c < 64 ? __builtin_amdgcn_readlane(my_blk, c) : btab[c];
-      kpos = kj;
       ok = c * KV_BLOCK + kj < P;
+      kpos = ok ? kj : 0;
     } else {
       const int e = (c - nbp) * KV_BLOCK + kj;
-      const int sl = e < E ? a.extra_slot[(int64_t)i * a.max_extra + e] : -1;
+      const int sl = a.extra_slot[(int64_t)i * a.max_extra + min(e, E - 1)];
       blk = sl >> 4;
       kpos = sl & 15;
-      ok = sl >= 0;
+      ok = e < E && sl >= 0;
     }
-    ok = ok && blk >= 0 && blk < a.pool_blocks;
-    off = pool_off(ok ? blk : 0, a.pool_blocks, a.layer, 0, H, head, ok ? kpos : 0) + dq;
+    const bool in_pool = blk >= 0 && blk < a.pool_blocks;
+    ok = ok && in_pool;
+    off = pool_off(in_pool ? blk : 0, a.pool_blocks, a.layer, 0, H, head, in_pool ? kpos : 0) + dq;
   };
 
   float m_run = -INFINITY, l_run = 0.f, acc[16];
@@ -318,21 +327,11 @@ __global__ __launch_bounds__(256) void attn_extend_wave_kernel(ExtendAttnArgs a)
   };
   // private keys that fit one chunk (a decode step's own key) are requested
   // first, with no dependent round trip after the prefix's last chunk, and
-  // reduced last; only the lanes of real keys load
+  // reduced last
   const bool x1 = E > 0 && E <= KV_BLOCK;
   Row16<T> kX, vX;
   bool okX = false;
-  if (x1) {
-    int64_t off;
-    locate(nbp, off, okX);
-    if (okX) {
-      fetch16<T>(pool + off, kX);
-      fetch16<T>(pool + off + voff, vX);
-    } else {
-#pragma unroll
-      for (int j = 0; j < (int)sizeof(T); ++j) kX.v[j] = vX.v[j] = make_uint4(0, 0, 0, 0);
-    }
-  }
+  if (x1) fetch_chunk(nbp, kX, vX, okX);
   const int nloop = x1 ? nbp : nch;
   // two register buffers: chunk c + 1 loads while chunk c is reduced
   Row16<T> kA, vA, kB, vB;

@@ -22,6 +22,12 @@ pytestmark = pytest.mark.gpu
 BPG = 8  # pool blocks owned by each game / root in these tests (128 positions)
 
 
+def nan_pool(eng, n_blocks):
+    """A KV pool whose unwritten memory holds NaN patterns (0xff bytes): a
+    slot that is not visible to a token must not reach its result."""
+    return eng.new_kv_pool(n_blocks).fill_(255)
+
+
 def check(got, ref, tol, what):
     lg = got.logits.cpu().numpy()
     dl = float(np.abs(lg - ref["logits"]).max())
@@ -48,7 +54,7 @@ def test_decode_steps_match_full_recompute(tiny, mode, tol, cuda):
     lens = rng.integers(1, 70, B).astype(np.int32)
     seqs = [list(rng.integers(0, 1968, n)) for n in lens]
     eng = Engine(cfg, sd, mode=mode)
-    pool = eng.new_kv_pool(B * BPG + 3)
+    pool = nan_pool(eng, B * BPG + 3)
     # game b owns blocks 3 + b * BPG ...: a non-contiguous, non-zero layout
     table = torch.tensor([[3 + b * BPG + j for j in range(BPG)] for b in range(B)], dtype=torch.int32, device=cuda)
     words = np.concatenate([np.asarray(s, np.uint32) for s in seqs])
@@ -66,6 +72,36 @@ def test_decode_steps_match_full_recompute(tiny, mode, tol, cuda):
             seqs[b].append(int(new[b]))
         ref = oracle.forward_last([np.asarray(s, np.int64) for s in seqs])
         check(out, ref, tol, f"{mode} decode step {step}")
+    eng.close()
+
+
+def test_decode_long_games(tiny, cuda):
+    """Decode steps of games of up to 514 positions (33 pool blocks) beside
+    short ones, ragged last blocks over NaN-filled unwritten slots, against
+    the full recompute (bf16, 2e-2)."""
+    cfg, sd = tiny
+    rng = np.random.default_rng(8)
+    lens = np.array([270, 271, 286, 300, 417, 5, 100, 511, 33], np.int32)
+    B, bpg = len(lens), 33  # 528 positions per game
+    seqs = [list(rng.integers(0, 1968, n)) for n in lens]
+    eng = Engine(cfg, sd, mode="bfloat16")
+    pool = nan_pool(eng, B * bpg + 2)
+    table = torch.tensor([[2 + b * bpg + j for j in range(bpg)] for b in range(B)], dtype=torch.int32, device=cuda)
+    words = np.concatenate([np.asarray(s, np.uint32) for s in seqs])
+    eng.prefill(words, lens, kv_pool=pool, kv_block_table=table)
+    oracle = RefModel(cfg, sd, mode="bfloat16")
+    status = torch.full((1,), -1, dtype=torch.int32, device=cuda)
+    for step in range(3):
+        new = rng.integers(0, 1968, B)
+        cur = np.array([len(s) for s in seqs], np.int32)
+        slots = np.array([(2 + b * bpg + cur[b] // 16) * 16 + cur[b] % 16 for b in range(B)], np.int32)
+        out = eng.extend(new, cur, [1] * B, cur, table, slots[:, None], np.ones(B, np.int32), pool, status=status)
+        torch.cuda.synchronize()
+        assert int(status.item()) == 0
+        for b in range(B):
+            seqs[b].append(int(new[b]))
+        ref = oracle.forward_last([np.asarray(s, np.int64) for s in seqs])
+        check(out, ref, 2e-2, f"long decode step {step}")
     eng.close()
 
 
@@ -90,7 +126,7 @@ def test_tree_levels_match_full_recompute(tiny, mode, tol, prefix, kids, cuda):
     eng = Engine(cfg, sd, mode=mode)
     node_base = R * BPG  # node slots live in the blocks after the roots'
     n1 = sum(kids)
-    pool = eng.new_kv_pool(node_base + (3 * n1 + 15) // 16 + 1)
+    pool = nan_pool(eng, node_base + (3 * n1 + 15) // 16 + 1)
     table = torch.tensor([[r * BPG + j for j in range(BPG)] for r in range(R)], dtype=torch.int32, device=cuda)
     eng.prefill(np.concatenate([np.asarray(s, np.uint32) for s in roots]), np.array(prefix, np.int32),
                 kv_pool=pool, kv_block_table=table)
@@ -143,7 +179,7 @@ def test_mixed_batch_matches_full_recompute(tiny, mode, tol, new_sizes, cuda):
     seqs = [list(rng.integers(0, 1968, n)) for n in lens]
     eng = Engine(cfg, sd, mode=mode)
     n_games = B + 3
-    pool = eng.new_kv_pool(n_games * BPG + 1)
+    pool = nan_pool(eng, n_games * BPG + 1)
     table = torch.tensor([[g * BPG + j for j in range(BPG)] for g in range(n_games)], dtype=torch.int32,
                          device=cuda)
     eng.prefill(np.concatenate([np.asarray(s, np.uint32) for s in seqs]), lens, kv_pool=pool,
