@@ -20,10 +20,9 @@
 namespace {
 
 template <int NV>
-__device__ __forceinline__ void ln_row_store(const float4 (&v)[NV], int d,
-                                             const float* __restrict__ g,
-                                             const float* __restrict__ b, float eps, void* y,
-                                             int64_t row, int act_bf16) {
+__device__ __forceinline__ void ln_row_store_gb(const float4 (&v)[NV], int d, const float4 (&gg)[NV],
+                                                const float4 (&bb)[NV], float eps, void* y, int64_t row,
+                                                int act_bf16) {
   const int lane = threadIdx.x & 63;
   float s = 0.f;
 #pragma unroll
@@ -32,19 +31,17 @@ __device__ __forceinline__ void ln_row_store(const float4 (&v)[NV], int d,
   float q = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    float a = v[i].x - mean, bb = v[i].y - mean, c = v[i].z - mean, e = v[i].w - mean;
-    q += (a * a + bb * bb) + (c * c + e * e);
+    float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean, e = v[i].w - mean;
+    q += (a * a + b * b) + (c * c + e * e);
   }
   const float rstd = rsqrtf(wave_sum(q) / (float)d + eps);
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = (i * 64 + lane) * 4;
-    float4 gg = *reinterpret_cast<const float4*>(g + c);
-    float4 bb = *reinterpret_cast<const float4*>(b + c);
-    float o0 = (v[i].x - mean) * rstd * gg.x + bb.x;
-    float o1 = (v[i].y - mean) * rstd * gg.y + bb.y;
-    float o2 = (v[i].z - mean) * rstd * gg.z + bb.z;
-    float o3 = (v[i].w - mean) * rstd * gg.w + bb.w;
+    float o0 = (v[i].x - mean) * rstd * gg[i].x + bb[i].x;
+    float o1 = (v[i].y - mean) * rstd * gg[i].y + bb[i].y;
+    float o2 = (v[i].z - mean) * rstd * gg[i].z + bb[i].z;
+    float o3 = (v[i].w - mean) * rstd * gg[i].w + bb[i].w;
     if (act_bf16) {
       uint2 p;
       p.x = pack_bf16x2(o0, o1);
@@ -55,6 +52,28 @@ __device__ __forceinline__ void ln_row_store(const float4 (&v)[NV], int d,
           make_float4(o0, o1, o2, o3);
     }
   }
+}
+
+// this lane's gamma and beta (columns 4 (64 i + lane) .. +3)
+template <int NV>
+__device__ __forceinline__ void ln_load_gb(const float* __restrict__ g, const float* __restrict__ b,
+                                           float4 (&gg)[NV], float4 (&bb)[NV]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    gg[i] = *reinterpret_cast<const float4*>(g + (i * 64 + lane) * 4);
+    bb[i] = *reinterpret_cast<const float4*>(b + (i * 64 + lane) * 4);
+  }
+}
+
+template <int NV>
+__device__ __forceinline__ void ln_row_store(const float4 (&v)[NV], int d,
+                                             const float* __restrict__ g,
+                                             const float* __restrict__ b, float eps, void* y,
+                                             int64_t row, int act_bf16) {
+  float4 gg[NV], bb[NV];
+  ln_load_gb<NV>(g, b, gg, bb);
+  ln_row_store_gb<NV>(v, d, gg, bb, eps, y, row, act_bf16);
 }
 
 template <int NV>
@@ -108,7 +127,10 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(allie::EmbedArgs a) {
   ln_row_store<NV>(v, d, a.ln_g, a.ln_b, a.eps, a.x, t, a.act_bf16);
 }
 
-template <int NV>
+// ADD: 0 no addend, 1 add, 2 add and add2 (template arguments, so that the
+// row's loads are issued together: loads under a runtime condition each get
+// a wait of their own)
+template <int NV, int ADD>
 __global__ __launch_bounds__(256) void layernorm_kernel(allie::LNArgs a) {
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= a.rows_out) return;
@@ -127,31 +149,36 @@ __global__ __launch_bounds__(256) void layernorm_kernel(allie::LNArgs a) {
     return;
   }
   const int64_t src = a.row_idx ? (int64_t)a.row_idx[r] : r;
-  float4 v[NV];
+  float4 v[NV], gg[NV], bb[NV];
+  uint2 y[NV], z[NV];
+  ln_load_gb<NV>(a.g, a.b, gg, bb);  // with the row's loads, not after its sums
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = (i * 64 + lane) * 4;
     v[i] = *reinterpret_cast<const float4*>(a.h + src * d + c);
-    if (a.add) {  // h + bf16 GEMM output, in fp32 (exact widening)
-      const uint2 y = *reinterpret_cast<const uint2*>(reinterpret_cast<const bf16_t*>(a.add) + src * d + c);
-      v[i].x += bf2f(y.x & 0xffffu);
-      v[i].y += bf2f(y.x >> 16);
-      v[i].z += bf2f(y.y & 0xffffu);
-      v[i].w += bf2f(y.y >> 16);
-      if (a.add2) {
-        const uint2 z = *reinterpret_cast<const uint2*>(reinterpret_cast<const bf16_t*>(a.add2) + src * d + c);
-        v[i].x += bf2f(z.x & 0xffffu);
-        v[i].y += bf2f(z.x >> 16);
-        v[i].z += bf2f(z.y & 0xffffu);
-        v[i].w += bf2f(z.y >> 16);
-      }
+    if constexpr (ADD >= 1) y[i] = *reinterpret_cast<const uint2*>(reinterpret_cast<const bf16_t*>(a.add) + src * d + c);
+    if constexpr (ADD >= 2) z[i] = *reinterpret_cast<const uint2*>(reinterpret_cast<const bf16_t*>(a.add2) + src * d + c);
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    if constexpr (ADD >= 1) {  // h + bf16 GEMM output, in fp32 (exact widening)
+      v[i].x += bf2f(y[i].x & 0xffffu);
+      v[i].y += bf2f(y[i].x >> 16);
+      v[i].z += bf2f(y[i].y & 0xffffu);
+      v[i].w += bf2f(y[i].y >> 16);
+    }
+    if constexpr (ADD >= 2) {
+      v[i].x += bf2f(z[i].x & 0xffffu);
+      v[i].y += bf2f(z[i].x >> 16);
+      v[i].z += bf2f(z[i].y & 0xffffu);
+      v[i].w += bf2f(z[i].y >> 16);
     }
   }
   if (a.h_out) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) *reinterpret_cast<float4*>(a.h_out + src * d + (i * 64 + lane) * 4) = v[i];
   }
-  ln_row_store<NV>(v, d, a.g, a.b, a.eps, a.y, r, a.act_bf16);
+  ln_row_store_gb<NV>(v, d, gg, bb, a.eps, a.y, r, a.act_bf16);
 }
 
 // dst row r = src row idx[r], 16 bytes per thread
@@ -227,7 +254,11 @@ hipError_t launch_layernorm(const LNArgs& a, hipStream_t st) {
   if ((a.add && !a.act_bf16) || (a.add2 && !a.add)) return hipErrorInvalidValue;
   if (a.rows_out == 0) return hipSuccess;
   dim3 grid((a.rows_out + 3) / 4);
-  ALLIE_NV_SWITCH(a.d / 256, hipLaunchKernelGGL(layernorm_kernel<NV>, grid, dim3(256), 0, st, a));
+  switch (a.add ? (a.add2 ? 2 : 1) : 0) {
+    case 0: ALLIE_NV_SWITCH(a.d / 256, hipLaunchKernelGGL((layernorm_kernel<NV, 0>), grid, dim3(256), 0, st, a)); break;
+    case 1: ALLIE_NV_SWITCH(a.d / 256, hipLaunchKernelGGL((layernorm_kernel<NV, 1>), grid, dim3(256), 0, st, a)); break;
+    default: ALLIE_NV_SWITCH(a.d / 256, hipLaunchKernelGGL((layernorm_kernel<NV, 2>), grid, dim3(256), 0, st, a)); break;
+  }
   return hipGetLastError();
 }
 
