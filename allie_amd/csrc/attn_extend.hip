@@ -509,12 +509,9 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
     // slot by its own lanes: the softmax starts from that key, and the
     // columns carry only the other private keys (a tree level's own keys
     // would otherwise be one column per query).
-    const int E = q_ok ? a.n_extra[qi] : 0;
-    int sl = -1;
-    if (E >= 1 && E <= a.max_extra) {
-      const int v = a.extra_slot[(int64_t)qi * a.max_extra + E - 1];
-      sl = (v >= 0 && (v >> 4) < a.pool_blocks) ? v : -1;
-    }
+    // (self_slot: the prepare step's copy, one dependent load instead of two)
+    const int v = q_ok ? a.self_slot[qi] : -1;
+    const int sl = (v >= 0 && (v >> 4) < a.pool_blocks) ? v : -1;
     const bool has_self = sl >= 0;
     const bf16_t* row = lbase + (int64_t)(has_self ? sl >> 4 : 0) * bstride + (sl & 15) * HD;
     float sdot = 0.f;
@@ -1070,6 +1067,7 @@ hipError_t launch_attn_extend_fan(const ExtendAttnArgs& a, int g0, int g1, int w
 }
 
 hipError_t launch_attn_extend_tree(const ExtendAttnArgs& a, hipStream_t st) {
+  if (!a.self_slot) return hipErrorInvalidValue;
   if (!a.act_bf16 || a.tiles == nullptr) return hipErrorInvalidValue;
   if (a.n_tiles == 0) return hipSuccess;
   if (a.tile_q == 128)  // 8 waves, two chunks in flight

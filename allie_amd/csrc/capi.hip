@@ -1087,6 +1087,7 @@ int extend_run(allie_model* m, const ExtendPlan& plan, const ExtendWS& w, const 
   xa.scale = 0.125f;  // 1 / sqrt(64)
   xa.out = w.attn;
   xa.act_bf16 = act;
+  xa.self_slot = w.self_slot;  // written by the prepare step above
 
   // one-token groups (decode steps) [0, n_dec) stream their keys with one
   // wave per (token, head), the games with the most keys first (bf16)
