@@ -427,19 +427,21 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
   auto valid_blk = [&](int v) { return (v >= 0 && v < a.pool_blocks) ? v : -1; };
   auto pblk = [&](int bi) { return bi < 64 ? s_blk[bi] : (bi < nbp ? valid_blk(btab[bi]) : -1); };
 
-  // ---- loads: block table, queries, the private keys' slots --------------
-  if (tid < 64) {  // the table row is read before the prefix length is known
-    const int v = tid < a.max_blocks ? btab[tid] : -1;
-    s_blk[tid] = tid < nbp ? valid_blk(v) : -1;
-  }
+  // ---- loads: block table, queries, positions, own slots ----------------
+  // (issued together, none under a condition: a load under one gets a wait
+  // of its own before the next is issued)
+  const int bt_v = btab[min(tid & 63, max(a.max_blocks - 1, 0))];  // read before the prefix length is known
   const int qloc = wave * 16 + lq;  // tile-local query of this lane
   const bool q_ok = qloc < ntok;
   const int qi = q_first + (q_ok ? qloc : 0);
-  const int lim = q_ok ? min(P, a.pos[qi]) : 0;
+  const int pos_qi = a.pos[qi];
+  const int self_v = a.self_slot[qi];
   bf16x8_t qf[2];  // B operand of S^T = K Q^T: query lq, dims 32 ks + 8 lg .. +7
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks)
     qf[ks] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(qkv + (int64_t)qi * ld + head * HD + 32 * ks + 8 * lg));
+  if (tid < 64) s_blk[tid] = (tid < nbp && tid < a.max_blocks) ? valid_blk(bt_v) : -1;
+  const int lim = q_ok ? min(P, pos_qi) : 0;
 
   // columns of extra indices [eb, eb + TREE_EB): wave h < NH builds tokens
   // 64 h .. 64 h + 63 (lane = token); a run never crosses two halves.  Ends
@@ -510,8 +512,7 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
     // columns carry only the other private keys (a tree level's own keys
     // would otherwise be one column per query).
     // (self_slot: the prepare step's copy, one dependent load instead of two)
-    const int v = q_ok ? a.self_slot[qi] : -1;
-    const int sl = (v >= 0 && (v >> 4) < a.pool_blocks) ? v : -1;
+    const int sl = (q_ok && self_v >= 0 && (self_v >> 4) < a.pool_blocks) ? self_v : -1;
     const bool has_self = sl >= 0;
     const bf16_t* row = lbase + (int64_t)(has_self ? sl >> 4 : 0) * bstride + (sl & 15) * HD;
     float sdot = 0.f;
