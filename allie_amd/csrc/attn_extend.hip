@@ -399,13 +399,14 @@ ALLIE_DEV int kswz(int r) { return (r >> 1) & 7; }
 template <int NW, int DEPTH>
 __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttnArgs a) {
   constexpr int TQ = NW * 16, NT = NW * 64, PER = 512 / NT;  // PER: 16-byte K (and V) pieces per thread per chunk
+  static_assert(NT >= TREE_MAX_BLOCKS, "one thread per staged block id");
   constexpr int NH = TQ / 64;                               // 64-token halves (column builder waves)
   constexpr int MAXC = TQ * TREE_EB;
   __shared__ __attribute__((aligned(1024))) uint16_t sK[KT * HD];
   __shared__ __attribute__((aligned(1024))) uint16_t sV[KT * HD];
   __shared__ int32_t c_slot[MAXC + 64];   // column -> pool slot (-1: padding)
   __shared__ __attribute__((aligned(16))) uint32_t c_rng[MAXC + 64];  // column -> tile-local queries [lo, hi): lo | hi << 16
-  __shared__ int32_t s_blk[64];           // the prefix's first 64 pool blocks (-1: skipped)
+  __shared__ int32_t s_blk[TREE_MAX_BLOCKS];  // the prefix's pool blocks (-1: skipped)
   __shared__ int32_t s_tot[NH];
 
   const int head = blockIdx.y;
@@ -425,12 +426,17 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
   const int32_t* btab = a.prefix_blocks + (int64_t)g * a.max_blocks;
   const int nbp = min((P + KV_BLOCK - 1) / KV_BLOCK, a.max_blocks);  // blocks the prefix reads
   auto valid_blk = [&](int v) { return (v >= 0 && v < a.pool_blocks) ? v : -1; };
-  auto pblk = [&](int bi) { return bi < 64 ? s_blk[bi] : (bi < nbp ? valid_blk(btab[bi]) : -1); };
+  // (from LDS only: a global load in the chunk loop, even one under a
+  // condition never met, would make the wait before each staging cover the
+  // chunks in flight)
+  auto pblk = [&](int bi) { return bi < nbp ? s_blk[bi] : -1; };
 
   // ---- loads: block table, queries, positions, own slots ----------------
   // (issued together, none under a condition: a load under one gets a wait
   // of its own before the next is issued)
-  const int bt_v = btab[min(tid & 63, max(a.max_blocks - 1, 0))];  // read before the prefix length is known
+  // (the table row is read before the prefix length is known; no table: a
+  // harmless read)
+  const int bt_v = *(a.max_blocks > 0 ? btab + min(tid, a.max_blocks - 1) : a.group_start + g);
   const int qloc = wave * 16 + lq;  // tile-local query of this lane
   const bool q_ok = qloc < ntok;
   const int qi = q_first + (q_ok ? qloc : 0);
@@ -440,7 +446,7 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks)
     qf[ks] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(qkv + (int64_t)qi * ld + head * HD + 32 * ks + 8 * lg));
-  if (tid < 64) s_blk[tid] = (tid < nbp && tid < a.max_blocks) ? valid_blk(bt_v) : -1;
+  if (tid < TREE_MAX_BLOCKS) s_blk[tid] = (tid < nbp && tid < a.max_blocks) ? valid_blk(bt_v) : -1;
   const int lim = q_ok ? min(P, pos_qi) : 0;
 
   // columns of extra indices [eb, eb + TREE_EB): wave h < NH builds tokens
@@ -1068,7 +1074,7 @@ hipError_t launch_attn_extend_fan(const ExtendAttnArgs& a, int g0, int g1, int w
 }
 
 hipError_t launch_attn_extend_tree(const ExtendAttnArgs& a, hipStream_t st) {
-  if (!a.self_slot) return hipErrorInvalidValue;
+  if (!a.self_slot || a.max_blocks > TREE_MAX_BLOCKS) return hipErrorInvalidValue;
   if (!a.act_bf16 || a.tiles == nullptr) return hipErrorInvalidValue;
   if (a.n_tiles == 0) return hipSuccess;
   if (a.tile_q == 128)  // 8 waves, two chunks in flight

@@ -213,7 +213,9 @@ hipError_t launch_attn_extend_wave(const ExtendAttnArgs& a, hipStream_t st);
 // order[0 .. n) of the one-token groups 0 .. n - 1, most keys first
 hipError_t launch_decode_order(const ExtendAttnArgs& a, int n, int32_t* order, hipStream_t st);
 // MFMA tiles of tile_q queries sharing a group's prefix, private keys as
-// columns (bf16); needs tiles
+// columns (bf16); needs tiles and self_slot, and a block table of at most
+// TREE_MAX_BLOCKS blocks (staged in LDS)
+constexpr int TREE_MAX_BLOCKS = 256;
 hipError_t launch_attn_extend_tree(const ExtendAttnArgs& a, hipStream_t st);
 // Groups g0 .. of at most FAN_MAX_Q tokens each (bf16): one workgroup of
 // fan_waves(max_blocks) waves per (group, head), the waves splitting the

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from allie_amd import config, weights
+from allie_amd import capi, config, weights
 from allie_amd.engine import Engine
 from oracle.model_ref import RefModel, policy_summary
 
@@ -249,4 +249,10 @@ def test_extend_status_flags(tiny, cuda):
     eng.extend([5], [5000], [1], [3], np.full((1, 2), -1, np.int32), [[1]], [1], pool, status=status)
     torch.cuda.synchronize()
     assert int(status.item()) & 4 and int(status.item()) & 2
+    # a group of 17 tokens (tree kernel) over a table wider than 256 blocks:
+    # refused on the host before any launch
+    n = 17
+    with pytest.raises(capi.AllieError, match="block tables of at most 256"):
+        eng.extend(np.full(n, 5), np.arange(n, dtype=np.int32), [n], [0], np.zeros((1, 257), np.int32),
+                   np.arange(n, dtype=np.int32)[:, None], np.ones(n, np.int32), pool, status=status)
     eng.close()
