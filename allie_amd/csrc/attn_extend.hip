@@ -835,15 +835,11 @@ __global__ __launch_bounds__(512, 4) void attn_extend_fan_kernel(ExtendAttnArgs 
   };
 
   const int nch = (max(P, 0) + FAN_CHUNK - 1) / FAN_CHUNK;
-  // pool block of (chunk c, block b); -1: skipped
-  auto table_entry = [&](int c, int b) {
-    const int bi = c * 4 + b;
-    int v = -1;
-    if (bi < a.max_blocks && bi * KV_BLOCK < P) v = btab[bi];
-    return (v >= 0 && v < a.pool_blocks) ? v : -1;
-  };
-  // lane j holds block j % 4 of the wave's chunk j / 4 (its first 16 chunks);
-  // the table row is read before the prefix length is known
+  // lane j holds block j % 4 of the wave's chunk j / 4: a wave has at most
+  // 16 chunks (FAN_MAX_BLOCKS), so the chunk loop makes no global load of its
+  // own (one there would make the compiler's wait before the chunk's loads
+  // cover every load issued before them); the table row is read before the
+  // prefix length is known
   int bt;
   {
     const int bi = (wave + W * (lane >> 2)) * 4 + (lane & 3);
@@ -875,7 +871,7 @@ __global__ __launch_bounds__(512, 4) void attn_extend_fan_kernel(ExtendAttnArgs 
     int blk[4];
 #pragma unroll
     for (int b = 0; b < 4; ++b)
-      blk[b] = __builtin_amdgcn_readfirstlane(n < 16 ? __builtin_amdgcn_readlane(bt, 4 * n + b) : table_entry(c, b));
+      blk[b] = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(bt, 4 * n + b));
     // V rows by DMA: instruction t, lane i fills row r = 8 t + i / 8 at
     // 16-byte position i % 8 (chunk (i % 8) ^ (2 ((r >> 1) & 1)); the swizzle
     // bit of r comes from i alone), from block t / 2; rows past the prefix or
@@ -1068,6 +1064,7 @@ hipError_t launch_attn_extend_wave(const ExtendAttnArgs& a, hipStream_t st) {
 hipError_t launch_attn_extend_fan(const ExtendAttnArgs& a, int g0, int g1, int waves, hipStream_t st) {
   if (!a.act_bf16 || g1 > a.n_groups || waves > 8) return hipErrorInvalidValue;
   const int W = waves > 0 ? waves : fan_waves(a.max_blocks);
+  if ((a.max_blocks + 3) / 4 > 16 * W) return hipErrorInvalidValue;  // a wave's chunks: at most 16
   const size_t lds = (size_t)W * (FAN_TILE * 2 + 32 * 4);
   if (g1 > g0) launch_timed(attn_extend_fan_kernel, dim3(g1 - g0, a.n_head), dim3(64 * W), (uint32_t)lds, st, a, g0);
   return hipGetLastError();

@@ -1005,6 +1005,9 @@ int extend_check(const allie_model* m, const int32_t* ids, const int32_t* pos, i
   if (p.max_rest > FAN_MAX_Q && max_blocks > TREE_MAX_BLOCKS)
     return fail(ALLIE_ERR_ARG, "groups of more than %d tokens take block tables of at most %d blocks (got %d)",
                 FAN_MAX_Q, TREE_MAX_BLOCKS, max_blocks);
+  if (p.max_rest > 1 && max_blocks > FAN_MAX_BLOCKS)
+    return fail(ALLIE_ERR_ARG, "groups of several tokens take block tables of at most %d blocks (got %d)",
+                FAN_MAX_BLOCKS, max_blocks);
   for (int g = p.n1; g < n_groups; ++g)
     p.n_tiles += (group_start_host[g + 1] - group_start_host[g] + p.tile_q - 1) / p.tile_q;
   *plan = p;

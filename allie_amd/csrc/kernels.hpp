@@ -221,6 +221,7 @@ hipError_t launch_attn_extend_tree(const ExtendAttnArgs& a, hipStream_t st);
 // fan_waves(max_blocks) waves per (group, head), the waves splitting the
 // prefix's 64-key chunks
 constexpr int FAN_MAX_Q = 16;
+constexpr int FAN_MAX_BLOCKS = 512;  // block-table width: 16 chunks of 4 blocks per wave at 8 waves
 inline int fan_waves(int max_blocks) {
   const int ch = (max_blocks * KV_BLOCK + 63) / 64;
   return ch < 1 ? 1 : (ch > 8 ? 8 : ch);
