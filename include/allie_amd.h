@@ -186,9 +186,10 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
  * status (device int32[1], optional) is written with 1 a token's n_extra
  * outside [1, max_extra], 2 a block id or slot outside the pool, 4 a position
  * outside the model's positions; keys in bad blocks are skipped, never read.
- * Groups may hold at most 16384 tokens; a batch with a group of more than 16
- * tokens takes block tables of at most 256 blocks (max_blocks, 4096
- * positions; ALLIE_ERR_ARG otherwise).  A new game's whole prefix of P
+ * Groups may hold at most 16384 tokens; a batch with a group of several
+ * tokens after its leading one-token groups takes block tables of at most 512
+ * blocks (max_blocks), and of at most 256 blocks (4096 positions) with a
+ * group of more than 16 tokens (ALLIE_ERR_ARG otherwise).  A new game's whole prefix of P
  * tokens is one group with prefix_len P over the game's own blocks, token t
  * at pos t with its own slot (position t) as its only extra: every layer
  * writes the P keys before attention, and token t sees positions 0..t.  A
