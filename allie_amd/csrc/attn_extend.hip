@@ -676,7 +676,10 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
   };
 
   // two chunks in flight: chunk j + 2 loads into the registers chunk j was
-  // staged from while j is multiplied
+  // staged from while j is multiplied.  Every fetch in the loop is
+  // unconditional (past the last chunk it re-reads the last, never staged):
+  // a load under a condition makes the compiler's wait before the next
+  // multiply cover the chunk just requested
   uint4 kA[PER], vA[PER], kB[PER], vB[PER];
   bool oA[PER], oB[PER];
   __syncthreads();  // s_blk is in
@@ -693,13 +696,13 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
         __syncthreads();  // every wave is done with the previous chunk
         stage(kA, vA, oA);
         __syncthreads();
-        if (j + 2 < nch) fetch(j + 2, ncp, kA, vA, oA);
+        fetch(min(j + 2, nch - 1), ncp, kA, vA, oA);  // past the last: a re-read never staged
         if (wave_busy) compute(j, ncp);
         if (j + 1 >= nch) break;
         __syncthreads();
         stage(kB, vB, oB);
         __syncthreads();
-        if (j + 3 < nch) fetch(j + 3, ncp, kB, vB, oB);
+        fetch(min(j + 3, nch - 1), ncp, kB, vB, oB);
         if (wave_busy) compute(j + 1, ncp);
       }
     } else {
@@ -707,7 +710,7 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
         __syncthreads();
         stage(kA, vA, oA);
         __syncthreads();
-        if (j + 1 < nch) fetch(j + 1, ncp, kA, vA, oA);
+        fetch(min(j + 1, nch - 1), ncp, kA, vA, oA);
         if (wave_busy) compute(j, ncp);
       }
     }
