@@ -16,6 +16,7 @@ medium model at 512 positions take 48 GiB of the 288 GiB HBM).
 from __future__ import annotations
 
 from dataclasses import dataclass, field
+from typing import Callable, Optional
 
 import numpy as np
 
@@ -48,6 +49,23 @@ class GameQueue:
         total = np.minimum(total, self.cap)
         prefixes = [self.rng.integers(0, NUM_CHESS_MOVES, int(p)).astype(np.int32) for p in P]
         return prefixes, P.astype(np.int32), total.astype(np.int32)
+
+
+@dataclass
+class Check:
+    """One recorded forward row: the first ``n`` tokens of ``game`` (a slot's
+    game, appended to in place) and the greedy move predicted after them;
+    ``out`` holds the row's logits, raw logits, value and time when the
+    batcher was asked to keep them."""
+
+    game: list
+    n: int
+    move: int
+    out: Optional[dict] = None
+
+    @property
+    def ids(self) -> list:
+        return self.game[: self.n]
 
 
 class PinnedUploader:
@@ -97,9 +115,14 @@ class ContinuousBatcher:
 
     ``record=True`` (tests) keeps each slot's game on the host and every
     (game so far, greedy move predicted for it) pair in ``checks``; it reads
-    the moves back every step, so it synchronises the stream."""
+    the moves back every step, so it synchronises the stream.  ``keep``
+    (with ``record``), given a row's context length and whether the row is a
+    new game's first move, says whether to keep that row's logits, raw
+    logits, value and time as well; a step with such a row computes the full
+    logits."""
 
-    def __init__(self, engine, n_slots: int = 1024, queue: GameQueue | None = None, record: bool = False):
+    def __init__(self, engine, n_slots: int = 1024, queue: GameQueue | None = None, record: bool = False,
+                 keep: Optional[Callable[[int, bool], bool]] = None):
         import torch
 
         self.torch = torch
@@ -125,8 +148,9 @@ class ContinuousBatcher:
         self.decode_keys = 0   # keys attended by the running games' one-token steps
         self.decoded = 0       # one-token steps (running games)
         self.record = record
+        self.keep = keep if record else None
         self.games = [[] for _ in range(n_slots)]
-        self.checks = []  # (game so far, predicted next move) when recording
+        self.checks: list[Check] = []  # when recording
         self.pending = {}  # slot -> (prefix ids, total length) to start next step
         self._draw(np.arange(n_slots))
 
@@ -167,12 +191,14 @@ class ContinuousBatcher:
         gs_l = gs_t.long()
         ids = torch.cat([self.next_tok.index_select(0, gs_l[:nR]), idsp_t])
         fed = ids[:nR].cpu().numpy() if self.record else None
+        # outputs: running games' next moves, new games' first moves (last prefix token)
+        last = np.concatenate([np.arange(nR), nR + np.cumsum(Ps) - 1]).astype(np.int32) if pend else None
+        ctx = np.concatenate([self.cur[R] + 1, Ps]) if pend else self.cur[R] + 1  # context of each output row
+        kept = [j for j, c in enumerate(ctx) if self.keep(int(c), j >= nR)] if self.keep else []
         out = self.eng.extend(ids, pos_t, [1] * nR + Ps.tolist(), pl_t, self.table.index_select(0, gs_l),
                               own_t[:, None], self.ones[:n] if n <= len(self.ones) else torch.ones(
                                   n, dtype=torch.int32, device=meta.device),
-                              self.pool, want_logits=False, status=self.status)
-        # outputs: running games' next moves, new games' first moves (last prefix token)
-        last = np.concatenate([np.arange(nR), nR + np.cumsum(Ps) - 1]).astype(np.int32) if pend else None
+                              self.pool, want_logits=bool(kept), want_raw_logits=bool(kept), status=self.status)
         if pend:
             last_t = self.up(last).long()
             self.next_tok.index_copy_(0, gs_l, out.top1.index_select(0, last_t))
@@ -180,12 +206,18 @@ class ContinuousBatcher:
             self.next_tok.index_copy_(0, gs_l, out.top1)
         if self.record:
             top = out.top1.cpu().numpy()
+            rows = {}
+            if kept:
+                sel = torch.as_tensor(last[kept] if pend else np.asarray(kept), device=out.top1.device).long()
+                host = {k: getattr(out, k).index_select(0, sel).cpu().numpy()
+                        for k in ("logits", "logits_raw", "value", "time")}
+                rows = {j: {k: v[q] for k, v in host.items()} for q, j in enumerate(kept)}
             for k, s in enumerate(R):
                 self.games[s].append(int(fed[k]))
-                self.checks.append((list(self.games[s]), int(top[k])))
+                self.checks.append(Check(self.games[s], len(self.games[s]), int(top[k]), rows.get(k)))
             for k, s in enumerate(pend):
-                self.games[s] = [int(x) for x in pre[k]]
-                self.checks.append((list(self.games[s]), int(top[last[nR + k]])))
+                self.games[s] = [int(x) for x in pre[k]]  # a new list: earlier checks keep the old game
+                self.checks.append(Check(self.games[s], len(self.games[s]), int(top[last[nR + k]]), rows.get(nR + k)))
         self.keys_read += int(self.cur[R].sum()) + nR + int((Ps * (Ps + 1) // 2).sum())
         self.decode_keys += int(self.cur[R].sum()) + nR
         self.decoded += nR

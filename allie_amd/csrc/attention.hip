@@ -7,18 +7,19 @@
 //
 // attn_varlen_seq_kernel -- one workgroup of 8 waves per (game, 4 heads), or per
 // (game, head) when there are fewer than 64 games.
-// A head's keys (bf16) and values (converted once to fp16, exact for bf16
-// values in fp16's range) of the whole game are staged in LDS (at most 512
-// tokens, 128 KiB); each wave then takes 32-query tiles in an order that
-// balances the causal work (tile t costs t + 1 key blocks) and waits for
-// the others only when the next head (loaded into registers meanwhile) is
-// staged.  Per 32-key block: S^T = K Q^T with MFMA 32x32x16 bf16, so a
+// A head's keys and values (bf16) of the whole game are staged in LDS (at
+// most 512 tokens, 128 KiB); each wave then takes 32-query tiles in an order
+// that balances the causal work (tile t costs t + 1 key blocks) and waits
+// for the others only when the next head (loaded into registers meanwhile)
+// is staged.  Per 32-key block: S^T = K Q^T with MFMA 32x32x16 bf16, so a
 // lane owns one query and 16 keys (the row max and sum need one exchange
 // with lane l ^ 32); online softmax in fp32 with exp2, the accumulator
-// rescaled only when some lane's running max grows; P goes to fp16 (11
-// significant bits against bf16's 8) and O^T += V^T P^T runs on MFMA
-// 32x32x16 f16, whose V^T fragments come straight from the row-major value
-// rows through gfx950's transposing LDS read (ds_read_b64_tr_b16).
+// rescaled only when some lane's running max grows.  As in torch's bf16
+// SDPA kernels, P = exp(s - max) enters the PV product rounded to bf16
+// (nearest even) while the row sum adds the unrounded fp32 P; O^T += V^T P^T
+// runs on MFMA 32x32x16 bf16, whose V^T fragments come straight from the
+// row-major value rows through gfx950's transposing LDS read
+// (ds_read_b64_tr_b16).
 //
 // Grid: (head group, game), the games in order of decreasing length
 // (seq_order_kernel, a counting sort) so that the longest start first.
@@ -37,18 +38,14 @@ constexpr int SEQ_HEADS = 4;       // heads per workgroup (the next one loads du
 constexpr int SEQ_FEW = 64;        // fewer games: one head per workgroup, so a batch of one
                                    // game still spreads over n_head workgroups
 
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef __fp16 fp16x4_ll __attribute__((__vector_size__(4 * sizeof(__fp16))));
-typedef __attribute__((address_space(3))) fp16x4_ll lds_f16x4_t;
-
-// two fp32 -> packed fp16 (round toward zero: exact for bf16 inputs in range)
-ALLIE_DEV uint32_t pk_f16(float a, float b) { return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b)); }
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
 
 __global__ __launch_bounds__(SEQ_WAVES * 64, 1) void attn_varlen_seq_kernel(AttnVarlenArgs a) {
   // K rows: 128 B, 16-byte chunk c of row r at c ^ ((r >> 1) & 7) (16
-  // consecutive rows reading one chunk hit distinct bank groups).  V rows
-  // (fp16): 128 B, 8-byte chunk j of row r at j ^ (4 ((r >> 1) & 1)) (the
-  // 4 x 16 blocks the transposing read takes hit distinct bank groups).
+  // consecutive rows reading one chunk hit distinct bank groups).  V rows:
+  // 128 B, 8-byte chunk j of row r at j ^ (4 ((r >> 1) & 1)) (the 4 x 16
+  // blocks the transposing read takes hit distinct bank groups).
   __shared__ __attribute__((aligned(1024))) uint16_t sK[SEQ_MAXN * HD];
   __shared__ __attribute__((aligned(1024))) uint16_t sV[SEQ_MAXN * HD];
 
@@ -88,13 +85,8 @@ __global__ __launch_bounds__(SEQ_WAVES * 64, 1) void attn_varlen_seq_kernel(Attn
       const int row = c >> 3, ch = c & 7;
       if (row >= npad) break;
       *reinterpret_cast<uint4*>(sK + row * HD + ((ch ^ ((row >> 1) & 7)) << 3)) = kv[i];
-      uint4 h;
-      h.x = pk_f16(bf2f(vv[i].x & 0xffffu), bf2f(vv[i].x >> 16));
-      h.y = pk_f16(bf2f(vv[i].y & 0xffffu), bf2f(vv[i].y >> 16));
-      h.z = pk_f16(bf2f(vv[i].z & 0xffffu), bf2f(vv[i].z >> 16));
-      h.w = pk_f16(bf2f(vv[i].w & 0xffffu), bf2f(vv[i].w >> 16));
       // 16 bytes = 8-byte chunks 2 ch, 2 ch + 1: the swizzle moves them together
-      *reinterpret_cast<uint4*>(sV + row * HD + ((ch ^ (((row >> 1) & 1) << 1)) << 3)) = h;
+      *reinterpret_cast<uint4*>(sV + row * HD + ((ch ^ (((row >> 1) & 1) << 1)) << 3)) = vv[i];
     }
   };
   const int hpw = (a.n_head + gridDim.x - 1) / gridDim.x;  // heads per workgroup (grid x = head groups)
@@ -164,29 +156,29 @@ __global__ __launch_bounds__(SEQ_WAVES * 64, 1) void attn_varlen_seq_kernel(Attn
         const float p0 = __builtin_amdgcn_exp2f(fmaf(st[r], c2, -mc));
         const float p1 = __builtin_amdgcn_exp2f(fmaf(st[r + 1], c2, -mc));
         lsum += p0 + p1;
-        pk[r >> 1] = pk_f16(p0, p1);
+        pk[r >> 1] = pack_bf16x2(p0, p1);
       }
       // ---- O^T += V^T P^T: k-step mm covers keys 16 mm + {4 g .. 4 g + 3,
       // 8 + 4 g .. 8 + 4 g + 3} (the S^T layout), identically for V^T -----
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) {
-        const f16x8_t pf = __builtin_bit_cast(f16x8_t, u32x4_t{pk[4 * mm], pk[4 * mm + 1], pk[4 * mm + 2], pk[4 * mm + 3]});
+        const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, u32x4_t{pk[4 * mm], pk[4 * mm + 1], pk[4 * mm + 2], pk[4 * mm + 3]});
 #pragma unroll
         for (int hb = 0; hb < 2; ++hb) {
-          fp16x4_ll lo, hi;
+          bf16x4_t lo, hi;
           {
             const int r0 = kb * 32 + 16 * mm + 4 * g + trow;  // rows of the two 4-key groups
             const int r1 = r0 + 8;
             const int j = hb * 8 + tchunk;
-            lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-                (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r0 * HD + ((j ^ (((r0 >> 1) & 1) << 2)) << 2)));
-            hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-                (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r1 * HD + ((j ^ (((r1 >> 1) & 1) << 2)) << 2)));
+            lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                (lds_bf16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r0 * HD + ((j ^ (((r0 >> 1) & 1) << 2)) << 2)));
+            hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                (lds_bf16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r1 * HD + ((j ^ (((r1 >> 1) & 1) << 2)) << 2)));
           }
-          const f16x8_t vf = __builtin_bit_cast(
-              f16x8_t, u32x4_t{__builtin_bit_cast(u32x2_t, lo).x, __builtin_bit_cast(u32x2_t, lo).y,
-                               __builtin_bit_cast(u32x2_t, hi).x, __builtin_bit_cast(u32x2_t, hi).y});
-          o[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[hb], 0, 0, 0);
+          const bf16x8_t vf = __builtin_bit_cast(
+              bf16x8_t, u32x4_t{__builtin_bit_cast(u32x2_t, lo).x, __builtin_bit_cast(u32x2_t, lo).y,
+                                __builtin_bit_cast(u32x2_t, hi).x, __builtin_bit_cast(u32x2_t, hi).y});
+          o[hb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[hb], 0, 0, 0);
         }
       }
     }

@@ -313,10 +313,13 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 4 : 1) void attn_extend_wave_
     const float alpha = exp2f(m_run - m_new);
     const float p = ok ? exp2f(s - m_new) : 0.f;
     l_run = l_run * alpha + ((lane & 3) == 0 ? p : 0.f);
+    // bf16: P enters the product with V rounded to bf16, the row sum takes
+    // it unrounded (torch's bf16 SDPA)
+    const float pv = sizeof(T) == 2 ? round_bf16(p) : p;
     float vv[16];
     widen16<T>(vr, vv);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) acc[j] = acc[j] * alpha + p * vv[j];
+    for (int j = 0; j < 16; ++j) acc[j] = acc[j] * alpha + pv * vv[j];
     m_run = m_new;
   };
   auto fetch_chunk = [&](int c, Row16<T>& kr, Row16<T>& vr, bool& ok) {
@@ -372,18 +375,15 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 4 : 1) void attn_extend_wave_
 }
 
 // ---------------------------------------------------------------------------
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef __fp16 fp16x4_ll __attribute__((__vector_size__(4 * sizeof(__fp16))));
-typedef __attribute__((address_space(3))) fp16x4_ll lds_f16x4_t;
-
-// two fp32 -> packed fp16 (round toward zero: exact for bf16 inputs in range)
-ALLIE_DEV uint32_t pk_f16(float a, float b) { return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b)); }
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
 
 // Tree kernel: a tile of TQ = 16 NW queries of one group (NW waves of 16
 // queries on 16x16x32 MFMAs) and one head.  Keys arrive in chunks of 64,
-// staged in LDS (K bf16 rows swizzled by kswz; V fp16, 8-byte chunk j of row
+// staged in LDS (K rows swizzled by kswz; V rows with 8-byte chunk j of row
 // r at j ^ (4 ((r >> 1) & 1)), read transposed), DEPTH chunks loading into
-// registers while one is multiplied.  First the
+// registers while one is multiplied.  P enters the PV product rounded to
+// bf16 and the row sum unrounded, as in torch's bf16 SDPA.  First the
 // group's prefix (query i sees positions below min(P, pos[i])), then the
 // tile's private keys other than the tokens' own as columns: for each extra
 // index e, a run of consecutive tokens whose e-th private key is the same
@@ -465,7 +465,9 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
 #pragma unroll
       for (int e = 0; e < TREE_EB; ++e) {
         const int ee = eb + e;
-        // the last private key is the token's own: it is taken from its qkv row
+        // the last private key is the token's own: its lanes read it from the
+        // pool at self_slot (below), never from qkv, whose K/V columns an
+        // extend leaves unwritten
         const int v = (ee < E - 1) ? a.extra_slot[(int64_t)i * a.max_extra + ee] : -1;
         sl[e] = (v >= 0 && (v >> 4) < a.pool_blocks) ? v : -1;
       }
@@ -583,12 +585,7 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
       const uint4 k4 = okf[it] ? kv[it] : make_uint4(0, 0, 0, 0);
       const uint4 v4 = okf[it] ? vv[it] : make_uint4(0, 0, 0, 0);
       *reinterpret_cast<uint4*>(sK + key * HD + ((c ^ kswz(key)) << 3)) = k4;
-      uint4 h;
-      h.x = pk_f16(bf2f(v4.x & 0xffffu), bf2f(v4.x >> 16));
-      h.y = pk_f16(bf2f(v4.y & 0xffffu), bf2f(v4.y >> 16));
-      h.z = pk_f16(bf2f(v4.z & 0xffffu), bf2f(v4.z >> 16));
-      h.w = pk_f16(bf2f(v4.w & 0xffffu), bf2f(v4.w >> 16));
-      *reinterpret_cast<uint4*>(sV + key * HD + ((c ^ (((key >> 1) & 1) << 1)) << 3)) = h;
+      *reinterpret_cast<uint4*>(sV + key * HD + ((c ^ (((key >> 1) & 1) << 1)) << 3)) = v4;
     }
   };
   auto compute = [&](int j, int ncp) {
@@ -649,8 +646,8 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
         }
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2)
-        pf[s2] = u32x4_t{pk_f16(p[2 * s2][0], p[2 * s2][1]), pk_f16(p[2 * s2][2], p[2 * s2][3]),
-                         pk_f16(p[2 * s2 + 1][0], p[2 * s2 + 1][1]), pk_f16(p[2 * s2 + 1][2], p[2 * s2 + 1][3])};
+        pf[s2] = u32x4_t{pack_bf16x2(p[2 * s2][0], p[2 * s2][1]), pack_bf16x2(p[2 * s2][2], p[2 * s2][3]),
+                         pack_bf16x2(p[2 * s2 + 1][0], p[2 * s2 + 1][1]), pack_bf16x2(p[2 * s2 + 1][2], p[2 * s2 + 1][3])};
       l_run = l_run * alpha + ls;
 #pragma unroll
       for (int db = 0; db < 4; ++db) o[db] *= alpha;
@@ -665,13 +662,13 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
       for (int db = 0; db < 4; ++db) {
         const int r0 = 32 * s2 + 4 * lg + trow, r1 = r0 + 16;
         const int jj = 4 * db + tchunk;
-        const fp16x4_ll lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-            (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r0 * HD + ((jj ^ (((r0 >> 1) & 1) << 2)) << 2)));
-        const fp16x4_ll hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-            (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r1 * HD + ((jj ^ (((r1 >> 1) & 1) << 2)) << 2)));
+        const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (lds_bf16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r0 * HD + ((jj ^ (((r0 >> 1) & 1) << 2)) << 2)));
+        const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (lds_bf16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r1 * HD + ((jj ^ (((r1 >> 1) & 1) << 2)) << 2)));
         const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
-        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, u32x4_t{l2.x, l2.y, h2.x, h2.y}),
-                                                       __builtin_bit_cast(f16x8_t, pf[s2]), o[db], 0, 0, 0);
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, u32x4_t{l2.x, l2.y, h2.x, h2.y}),
+                                                        __builtin_bit_cast(bf16x8_t, pf[s2]), o[db], 0, 0, 0);
       }
   };
 
@@ -736,13 +733,14 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
 // is requested at once.  A wave holds all of the group's queries in 16x16x32
 // MFMAs (S^T = K Q^T: key rows, query columns), loads its chunk's K
 // fragments straight into MFMA registers (a lane's key row segment is
-// contiguous), stages V as fp16 in its own LDS tile for the transposing
-// read, and keeps its own running max / sum / O.  The waves' partials merge
+// contiguous), stages V in its own LDS tile for the transposing read, and
+// keeps its own running max / sum / O.  P enters the PV products rounded to
+// bf16 and the row sums unrounded, as in torch's bf16 SDPA.  The waves' partials merge
 // through LDS and wave w finishes tokens w, w + W, ... (lane = head dim):
 // the private keys (ancestors, then the token itself) and the normalisation.
 // Everything a wave needs for its first tokens' private keys is loaded
 // before the prefix loop, so those loads overlap the prefix's.
-constexpr int FAN_CHUNK = 64, FAN_TILE = FAN_CHUNK * HD;  // fp16 V tile (8 KiB); later the fp32 16 x 64 partial
+constexpr int FAN_CHUNK = 64, FAN_TILE = FAN_CHUNK * HD;  // bf16 V tile (8 KiB); later the fp32 16 x 64 partial
 constexpr int FAN_PT = 2, FAN_PE = 2;  // tokens per wave x private keys per token loaded up front
 __device__ const uint4 fan_zero[64] = {};  // read in place of values outside the prefix
 
@@ -766,9 +764,6 @@ ALLIE_DEV float wave_sum_dpp(float v) {
   return (__int_as_float(__builtin_amdgcn_readlane(b, 0)) + __int_as_float(__builtin_amdgcn_readlane(b, 16))) +
          (__int_as_float(__builtin_amdgcn_readlane(b, 32)) + __int_as_float(__builtin_amdgcn_readlane(b, 48)));
 }
-
-// two bf16 (one word) -> two fp16 (exact for bf16 values in fp16's range)
-ALLIE_DEV uint32_t bf16x2_to_f16x2(uint32_t w) { return pk_f16(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u)); }
 
 ALLIE_DEV void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -828,7 +823,7 @@ __global__ __launch_bounds__(512, 4) void attn_extend_fan_kernel(ExtendAttnArgs 
         const float alpha = __builtin_amdgcn_exp2f((m - m_new) * c2);  // m = -inf: 0
         const float pe = __builtin_amdgcn_exp2f((sc - m_new) * c2);
         l = l * alpha + pe;
-        acc = acc * alpha + pe * bf2f(xv[t][e]);
+        acc = acc * alpha + round_bf16(pe) * bf2f(xv[t][e]);
         m = m_new;
       }
       xm[t] = m;
@@ -937,8 +932,8 @@ __global__ __launch_bounds__(512, 4) void attn_extend_fan_kernel(ExtendAttnArgs 
         }
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2)
-        pf[s2] = u32x4_t{pk_f16(p[2 * s2][0], p[2 * s2][1]), pk_f16(p[2 * s2][2], p[2 * s2][3]),
-                         pk_f16(p[2 * s2 + 1][0], p[2 * s2 + 1][1]), pk_f16(p[2 * s2 + 1][2], p[2 * s2 + 1][3])};
+        pf[s2] = u32x4_t{pack_bf16x2(p[2 * s2][0], p[2 * s2][1]), pack_bf16x2(p[2 * s2][2], p[2 * s2][3]),
+                         pack_bf16x2(p[2 * s2 + 1][0], p[2 * s2 + 1][1]), pack_bf16x2(p[2 * s2 + 1][2], p[2 * s2 + 1][3])};
       l_run = l_run * alpha + ls;
 #pragma unroll
       for (int db = 0; db < 4; ++db) o[db] *= alpha;
@@ -947,23 +942,22 @@ __global__ __launch_bounds__(512, 4) void attn_extend_fan_kernel(ExtendAttnArgs 
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the tile's DMA is done
     wave_lds_sync();
-    // O^T += V^T P^T: A = V^T rows (dims 16 db + lq) in fp16, k-slots as
-    // P^T's, read transposed: lane group lg reads keys 32 s + 4 lg + (lq >> 2)
-    // (and + 16)
+    // O^T += V^T P^T: A = V^T rows (dims 16 db + lq), k-slots as P^T's,
+    // read transposed: lane group lg reads keys 32 s + 4 lg + (lq >> 2) (and
+    // + 16)
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
         const int r0 = 32 * s2 + 4 * lg + (lq >> 2), r1 = r0 + 16;
         const int j = 4 * db + (lq & 3);
-        const fp16x4_ll lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-            (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r0 * HD + ((j ^ (((r0 >> 1) & 1) << 2)) << 2)));
-        const fp16x4_ll hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-            (lds_f16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r1 * HD + ((j ^ (((r1 >> 1) & 1) << 2)) << 2)));
+        const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (lds_bf16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r0 * HD + ((j ^ (((r0 >> 1) & 1) << 2)) << 2)));
+        const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (lds_bf16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r1 * HD + ((j ^ (((r1 >> 1) & 1) << 2)) << 2)));
         const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
-        const u32x4_t vf{bf16x2_to_f16x2(l2.x), bf16x2_to_f16x2(l2.y), bf16x2_to_f16x2(h2.x), bf16x2_to_f16x2(h2.y)};
-        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, vf), __builtin_bit_cast(f16x8_t, pf[s2]),
-                                                       o[db], 0, 0, 0);
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, u32x4_t{l2.x, l2.y, h2.x, h2.y}),
+                                                        __builtin_bit_cast(bf16x8_t, pf[s2]), o[db], 0, 0, 0);
       }
     wave_lds_sync();  // the transposing reads are done before the tile is written again
   }
@@ -1013,7 +1007,7 @@ __global__ __launch_bounds__(512, 4) void attn_extend_fan_kernel(ExtendAttnArgs 
         const float alpha = __builtin_amdgcn_exp2f((m - m_new) * c2);
         const float pe = __builtin_amdgcn_exp2f((sc - m_new) * c2);
         l = l * alpha + pe;
-        acc = acc * alpha + pe * bf2f(pool[kb + voff]);
+        acc = acc * alpha + round_bf16(pe) * bf2f(pool[kb + voff]);
         m = m_new;
       }
     }

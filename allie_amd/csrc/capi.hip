@@ -1002,10 +1002,12 @@ int extend_check(const allie_model* m, const int32_t* ids, const int32_t* pos, i
   }
   // queries per tree-kernel tile: 128 when some group is larger than 64
   p.tile_q = p.max_rest > 64 ? 128 : 64;
-  if (p.max_rest > FAN_MAX_Q && max_blocks > TREE_MAX_BLOCKS)
+  // the tree and fan kernels (bf16 modes only; the fp32 check mode runs every
+  // group on the wave kernel, which takes any table width) stage the table
+  if (m->act_bf16 && p.max_rest > FAN_MAX_Q && max_blocks > TREE_MAX_BLOCKS)
     return fail(ALLIE_ERR_ARG, "groups of more than %d tokens take block tables of at most %d blocks (got %d)",
                 FAN_MAX_Q, TREE_MAX_BLOCKS, max_blocks);
-  if (p.max_rest > 1 && max_blocks > FAN_MAX_BLOCKS)
+  if (m->act_bf16 && p.max_rest > 1 && max_blocks > FAN_MAX_BLOCKS)
     return fail(ALLIE_ERR_ARG, "groups of several tokens take block tables of at most %d blocks (got %d)",
                 FAN_MAX_BLOCKS, max_blocks);
   for (int g = p.n1; g < n_groups; ++g)

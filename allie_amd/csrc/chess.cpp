@@ -5,7 +5,7 @@
 // with push_uci, Game.legal_moves lists board.legal_moves as UCI
 // (src/modeling/data.py:51-61), and MCTS asks board.outcome()
 // (src/evaluation/decode.py:345-353).  python-chess is absent from the image;
-// allie_amd/movegen.py restates the rules in Python and fixes the order this
+// oracle/movegen.py restates the rules in Python and fixes the order this
 // file follows:
 //   not in check: pieces other than pawns by from-square descending (a1 = 0),
 //   targets descending; castling, king side first; pawn captures by

@@ -1,25 +1,38 @@
-"""bf16 parity at full depth, measured against the oracle's own floor.
+"""bf16 parity at full depth, and the fp32 check mode.
 
-Two faithful bf16-autocast implementations of a deep model do not agree to
-the last bit: every GEMM output is rounded to bf16, so a different summation
-order flips some roundings, and the flips compound through the layers.  The
-oracle measures this on the inputs of each check by running itself twice,
-with fp32 and with fp64 summation (same rounding points), and the GPU is
-held to the contract bar (2e-2) or to twice that floor, whichever is larger:
+bf16: two faithful bf16-autocast implementations of a deep model do not
+agree to the last bit: every GEMM output is rounded to bf16, so a different
+summation order flips some roundings, and the flips compound through the
+layers.  The oracle measures this on the inputs of each check by running
+itself twice, with fp32 and with fp64 summation (same rounding points).
+The GPU is held to the contract bar (2e-2) wherever that spread stays within
+it; only a quantity whose own spread exceeds 2e-2 (the 32-layer fp8 shape)
+is held to twice the spread instead, and the test prints which rule applied:
 
-* logits (after and before their final bf16 rounding), value and time:
-  max |GPU - oracle| <= max(2e-2, 2 * max |oracle64 - oracle32|), per
+* logits before their final bf16 rounding, value and time: max |GPU -
+  oracle| <= 2e-2 (or 2 x the spread where the spread > 2e-2), per
   quantity, and the median over games of the per-game logit error <= twice
-  the floor's median (the GPU is not systematically further off than a
+  the spread's median (the GPU is not systematically further off than a
   change of summation order);
+* the bf16-rounded logits (what the reference's autocast lm_head returns):
+  |GPU - oracle| <= that bound plus one bf16 ulp of the logit's magnitude
+  (two values less than the bound apart can round one ulp further apart:
+  0.0078 for |logit| in [1, 2), 0.0156 in [2, 4)); the rows beyond the bare
+  bound are counted and printed;
 * top-1 move: for EVERY game the GPU's pick is the oracle's first argmax,
   or a move whose oracle logit is within twice that bound of the maximum
-  (a near tie); exact agreement is required wherever the oracle's top-2
-  margin exceeds twice the bound.  Counts are printed.
+  (a near tie that the bar itself cannot order); exact agreement is
+  required wherever the oracle's top-2 margin exceeds twice the bound.
+  Counts are printed.
+
+fp32 (``check_fp32``): logits, value and time within 1e-4 of the fp32
+oracle, and the GPU's top-1 equal to the oracle's first argmax on every row
+whose oracle top-2 margin exceeds 1e-4 (rows within it are ties at the
+contract's resolution; their count is printed and is expected to be zero).
 
 Reference semantics: the last-token reads of Policy.score_full and
 MCTS.evaluate_node (src/evaluation/decode.py:204-226, 356-373) under bf16
-autocast (decode.py:74-78).
+autocast (decode.py:74-78), or in fp32 (evaluate.py:249).
 """
 from __future__ import annotations
 
@@ -40,6 +53,20 @@ def _per_game(x, y):
     return np.abs(np.asarray(x, np.float64) - np.asarray(y, np.float64)).reshape(len(x), -1).max(axis=1)
 
 
+def bf16_ulp(x) -> np.ndarray:
+    """Spacing of bf16 values at |x| (8 significant bits): 2^(e - 7) for
+    |x| in [2^e, 2^(e+1)); the smallest normal spacing at 0."""
+    a = np.abs(np.asarray(x, np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -126)))
+    return np.exp2(e - 7)
+
+
+def _bound(spread: np.ndarray) -> float:
+    """2e-2, or twice the oracle's own spread where that exceeds 2e-2."""
+    m = float(spread.max())
+    return BAR if m <= BAR else 2.0 * m
+
+
 def check_at_floor(label, got, ref, ref64, top1=None):
     """got: dict with logits, logits_raw, value, time ([n, ...] numpy);
     ref / ref64: oracle outputs (fp32 / fp64 summation) of the same rows;
@@ -51,13 +78,23 @@ def check_at_floor(label, got, ref, ref64, top1=None):
             continue
         e = _per_game(got[k_got], ref[k_ref])
         f = _per_game(ref64[k_ref], ref[k_ref])
-        bound = max(BAR, 2.0 * float(f.max()))
-        rows[k_got] = (e, f, bound)
-        print(f"{label} {k_got}: GPU max {e.max():.4f} median {np.median(e):.4f} (games > 2e-2: {(e > BAR).sum()}) | "
-              f"oracle fp64-vs-fp32 floor max {f.max():.4f} median {np.median(f):.4f} "
-              f"(games > 2e-2: {(f > BAR).sum()}) | bound {bound:.4f}", flush=True)
-    for k, (e, f, bound) in rows.items():
-        assert e.max() <= bound, (label, k, float(e.max()), bound)
+        g64 = _per_game(got[k_got], ref64[k_ref])
+        bound = _bound(f)
+        # the rounded logits may differ by one more bf16 ulp of their magnitude
+        if k_got == "logits":
+            d = np.abs(np.asarray(got[k_got], np.float64) - np.asarray(ref[k_ref], np.float64)) - bf16_ulp(ref[k_ref])
+            slack = np.maximum(d, 0.0).reshape(len(d), -1).max(axis=1)
+        else:
+            slack = e
+        rows[k_got] = (e, f, bound, slack)
+        rule = "plain 2e-2 bar" if bound == BAR else "floor rule (oracle spread > 2e-2)"
+        extra = " (+1 bf16 ulp of the logit)" if k_got == "logits" else ""
+        print(f"{label} {k_got}: GPU max {e.max():.4f} median {np.median(e):.4f} (rows > 2e-2: {(e > BAR).sum()} "
+              f"of {len(e)}) | GPU vs fp64-summation oracle max {g64.max():.4f} | oracle fp64-vs-fp32 spread max "
+              f"{f.max():.4f} median {np.median(f):.4f} (rows > 2e-2: {(f > BAR).sum()}) | bound {bound:.4f}{extra}, "
+              f"{rule}", flush=True)
+    for k, (e, f, bound, slack) in rows.items():
+        assert slack.max() <= bound, (label, k, float(e.max()), bound)
         if k.startswith("logits"):
             assert np.median(e) <= 2.0 * np.median(f) + 1e-6, (label, k, float(np.median(e)), float(np.median(f)))
     # top-1 against the oracle's logits
@@ -67,8 +104,8 @@ def check_at_floor(label, got, ref, ref64, top1=None):
     top1 = np.asarray(top1)
     if "logits" in rows:
         bound = rows["logits"][2]
-    else:  # only the GPU's moves are known: the floor alone sets the bound
-        bound = max(BAR, 2.0 * float(_per_game(ref64["logits"], ref["logits"]).max()))
+    else:  # only the GPU's moves are known: the spread alone sets the bound
+        bound = _bound(_per_game(ref64["logits"], ref["logits"]))
     tie = 2.0 * bound
     lg = np.asarray(ref["logits"], np.float64)[:, :1968]
     picked = lg[np.arange(len(top1)), top1]
@@ -80,4 +117,29 @@ def check_at_floor(label, got, ref, ref64, top1=None):
           f"<= {tie:.4f}", flush=True)
     assert (top1 >= 0).all() and (top1 < 1968).all()
     assert (gap <= tie).all(), (label, np.nonzero(gap > tie))
+    assert not (differ & decided).any(), (label, np.nonzero(differ & decided))
+
+
+FP32_BAR = 1e-4
+
+
+def check_fp32(label, got, ref, top1=None):
+    """fp32 check mode: got / ref as in check_at_floor (ref: the fp32
+    oracle's outputs of the same rows)."""
+    for k_got, k_ref in (("logits", "logits"), ("value", "value_logits"), ("time", "time_logits")):
+        if got.get(k_got) is None:
+            continue
+        e = _per_game(got[k_got], ref[k_ref])
+        print(f"{label} fp32 {k_got}: max {e.max():.2e} median {np.median(e):.2e} over {len(e)} rows "
+              f"(bar {FP32_BAR:g})", flush=True)
+        assert e.max() <= FP32_BAR, (label, k_got, float(e.max()))
+    ps = policy_summary(ref["logits"])
+    if top1 is None:
+        top1 = policy_summary(got["logits"])["top1"]
+    top1 = np.asarray(top1)
+    decided = ps["margin"] > FP32_BAR
+    differ = top1 != ps["top1"]
+    print(f"{label} fp32 top-1: {int(differ.sum())} of {len(top1)} differ from the oracle; "
+          f"{int((~decided).sum())} rows have an oracle top-2 margin <= {FP32_BAR:g}; smallest margin "
+          f"{ps['margin'].min():.2e}", flush=True)
     assert not (differ & decided).any(), (label, np.nonzero(differ & decided))

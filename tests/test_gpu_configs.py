@@ -2,8 +2,9 @@
 
 Each test runs one BASELINE config exactly as bench.py does and checks a
 sample of its outputs against the oracle's bf16 (or fp8-weight) mode under
-the floor rule of parity_floor.py (contract bar 2e-2, or twice what a change
-of summation order alone moves the oracle):
+the rule of parity_floor.py (contract bar 2e-2; only where a change of
+summation order alone moves the oracle by more, twice that), and the medium
+configs again in the fp32 check mode (1e-4, exact top-1):
 
 * C2: the whole 256-game medium batch in one prefill; 32 games checked, the
   10 longest among them;
@@ -11,9 +12,12 @@ of summation order alone moves the oracle):
   paged KV cache; every node's status and outputs are checked for range,
   4 nodes per level against a full recompute of their games, which is what
   MCTS.evaluate_node computes per leaf (src/evaluation/decode.py:356-373);
-* C4: 1,024 slots of continuous batching with eviction and refill; sampled
-  (game so far, greedy move) pairs against the oracle's first argmax of a
-  full recompute (Policy.decode_full, decode.py:109-113, 204-226);
+* C4: 1,024 slots of continuous batching with eviction and refill for 330
+  steps, so that contexts pass 256 cached keys (up to ~370 tokens); sampled
+  rows' logits, value, time and greedy move against a full recompute of
+  their games (Policy.score_full / decode_full, decode.py:109-113, 204-226),
+  spread over context lengths, with rows of more than 256 cached keys and
+  new games' first moves among them;
 * C5: the 2x shape (32 x 1280 x 20) with fp8 e4m3 per-channel weights on the
   C2 batch; 12 games, the 4 longest among them, against the oracle's fp8w
   mode.  Also reports top-1 agreement with the same model in bf16.
@@ -26,8 +30,8 @@ from allie_amd import config, weights
 from allie_amd.batcher import ContinuousBatcher, GameQueue
 from allie_amd.engine import Engine
 from allie_amd.tree import TreeExpansion, TreeLayout, node_path
-from oracle.model_ref import policy_summary
-from parity_floor import check_at_floor, oracle_pair
+from oracle.model_ref import RefModel, policy_summary
+from parity_floor import check_at_floor, check_fp32, oracle_pair
 
 pytestmark = pytest.mark.gpu
 
@@ -76,16 +80,18 @@ def test_c2_medium_at_size(medium, cuda):
     eng.close()
 
 
-def test_c3_tree_at_size(medium, cuda):
-    cfg, sd = medium
+def c3_rows(cfg, sd, mode, raw):
+    """The full C3 tree in one mode: every node's outputs checked for range,
+    4 nodes per level returned with their games."""
     lay = TreeLayout(n_roots=64, prefix_len=200, branching=8, depth=4)
-    eng = Engine(cfg, sd, mode="bfloat16")
+    eng = Engine(cfg, sd, mode=mode)
     tx = TreeExpansion(eng, lay, seed=3)
     tx.prefill_roots()
     rng = np.random.default_rng(0)
-    seqs, got = [], {"logits": [], "logits_raw": [], "value": [], "time": [], "top1": []}
+    keys = ["logits", "value", "time", "top1"] + (["logits_raw"] if raw else [])
+    seqs, got = [], {k: [] for k in keys}
     for k in range(1, lay.depth + 1):
-        out = tx.expand_level(k, want_logits=True, want_raw_logits=True)
+        out = tx.expand_level(k, want_logits=True, want_raw_logits=raw)
         torch.cuda.synchronize()
         assert int(tx.status.item()) == 0, k
         n = lay.level_size(k)
@@ -97,29 +103,106 @@ def test_c3_tree_at_size(medium, cuda):
             got[key].append(h[key])
         seqs += [np.asarray(node_path(lay, tx.prefixes, tx.levels, k, j), np.int64) for j in pick]
         del out
-    print(f"c3: {lay.n_nodes} nodes evaluated, {len(seqs)} checked", flush=True)
-    got = {k: np.concatenate(v) for k, v in got.items()}
+    print(f"c3 {mode}: {lay.n_nodes} nodes evaluated, {len(seqs)} checked", flush=True)
+    del tx
+    eng.close()
+    torch.cuda.empty_cache()
+    return {k: np.concatenate(v) for k, v in got.items()}, seqs
+
+
+def test_c3_tree_at_size(medium, cuda):
+    cfg, sd = medium
+    got, seqs = c3_rows(cfg, sd, "bfloat16", raw=True)
     ref, ref64 = oracle_pair(cfg, sd, "bfloat16", seqs)
     check_at_floor("c3", got, ref, ref64, top1=got["top1"])
-    eng.close()
 
 
-def test_c4_continuous_batching_at_size(medium, cuda):
-    cfg, sd = medium
-    eng = Engine(cfg, sd, mode="bfloat16")
-    cb = ContinuousBatcher(eng, n_slots=1024, queue=GameQueue(seed=4), record=True)
-    for _ in range(40):
+def c4_rows(cfg, sd, mode, steps, long_rows):
+    """C4 at size in one mode: 1,024 slots for ``steps`` steps; keeps one
+    running row per 16-token context bucket up to 256, one per 8-token
+    bucket above 256 cached keys (at most ``long_rows``), and a few new
+    games' first moves drawn across the run."""
+    eng = Engine(cfg, sd, mode=mode)
+    rng = np.random.default_rng(5)
+    seen, counts = set(), {"new": 0, "long": 0}
+
+    def keep(n, new):
+        if new:
+            if counts["new"] < 6 and rng.random() < 0.002:
+                counts["new"] += 1
+                return True
+            return False
+        b = ("s", n // 16) if n <= 257 else ("l", n // 8)
+        if b in seen or (b[0] == "l" and counts["long"] >= long_rows):
+            return False
+        seen.add(b)
+        counts["long"] += b[0] == "l"
+        return True
+
+    cb = ContinuousBatcher(eng, n_slots=1024, queue=GameQueue(seed=4), record=True, keep=keep)
+    for _ in range(steps):
         cb.step()
     torch.cuda.synchronize()
     assert int(cb.status.item()) == 0
     assert cb.games_started > 1024  # slots were evicted and refilled
-    idx = np.linspace(0, len(cb.checks) - 1, 24).astype(int)
-    seqs = [np.asarray(cb.checks[i][0], np.int64) for i in idx]
-    pred = np.array([cb.checks[i][1] for i in idx])
-    print(f"c4: {len(cb.checks)} greedy moves over {cb.games_started} games; {len(idx)} checked", flush=True)
-    ref, ref64 = oracle_pair(cfg, sd, "bfloat16", seqs)
-    check_at_floor("c4", {}, ref, ref64, top1=pred)
+    rows = [c for c in cb.checks if c.out is not None]
+    n_long = sum(c.n > 257 for c in rows)
+    print(f"c4 {mode}: {len(cb.checks)} greedy moves over {cb.games_started} games in {steps} steps; "
+          f"{len(rows)} rows checked (contexts {min(c.n for c in rows)}..{max(c.n for c in rows)}; {n_long} with "
+          f"more than 256 cached keys, {counts['new']} new games' first moves)", flush=True)
+    got = {k: np.stack([c.out[k] for c in rows]) for k in ("logits", "logits_raw", "value", "time")}
+    got["top1"] = np.array([c.move for c in rows])
+    seqs = [np.asarray(c.ids, np.int64) for c in rows]
+    del cb
     eng.close()
+    torch.cuda.empty_cache()
+    return got, seqs, n_long
+
+
+def test_c4_continuous_batching_at_size(medium, cuda):
+    cfg, sd = medium
+    got, seqs, n_long = c4_rows(cfg, sd, "bfloat16", steps=330, long_rows=12)
+    assert len(seqs) >= 24 and n_long >= 8
+    order = np.argsort([len(q) for q in seqs], kind="stable")  # similar lengths share a padded oracle batch
+    got = {k: v[order] for k, v in got.items()}
+    seqs = [seqs[i] for i in order]
+    ref, ref64 = oracle_pair(cfg, sd, "bfloat16", seqs)
+    check_at_floor("c4", got, ref, ref64, top1=got["top1"])
+
+
+def test_c2_medium_fp32_at_size(medium, cuda):
+    """C2 in the fp32 check mode (the reference evaluates in fp32,
+    src/evaluation/evaluate.py:249): the same 32 games at 1e-4."""
+    cfg, sd = medium
+    seqs, lens = c2_batch()
+    eng = Engine(cfg, sd, mode="float32")
+    r = eng.prefill(np.concatenate(seqs), lens)
+    torch.cuda.synchronize()
+    assert torch.isfinite(r.logits).all() and torch.isfinite(r.value).all()
+    pick = sample_games(lens, 10, 32)
+    got = host(r, torch.tensor(pick, device=r.value.device))
+    eng.close()
+    torch.cuda.empty_cache()
+    ref = RefModel(cfg, sd, mode="float32").forward_last([seqs[i].astype(np.int64) for i in pick])
+    check_fp32("c2", got, ref, top1=got["top1"])
+
+
+def test_c3_tree_fp32_at_size(medium, cuda):
+    """The full C3 tree in the fp32 check mode (a 57 GiB fp32 pool)."""
+    cfg, sd = medium
+    got, seqs = c3_rows(cfg, sd, "float32", raw=False)
+    ref = RefModel(cfg, sd, mode="float32").forward_last(seqs)
+    check_fp32("c3", got, ref, top1=got["top1"])
+
+
+def test_c4_continuous_batching_fp32_at_size(medium, cuda):
+    """C4's 1,024 slots in the fp32 check mode (a 96 GiB fp32 pool), 120
+    steps."""
+    cfg, sd = medium
+    got, seqs, _ = c4_rows(cfg, sd, "float32", steps=120, long_rows=0)
+    assert len(seqs) >= 12
+    ref = RefModel(cfg, sd, mode="float32").forward_last(seqs)
+    check_fp32("c4", got, ref, top1=got["top1"])
 
 
 def test_c5_fp8_weights_at_size(cuda):

@@ -256,3 +256,28 @@ def test_extend_status_flags(tiny, cuda):
         eng.extend(np.full(n, 5), np.arange(n, dtype=np.int32), [n], [0], np.zeros((1, 257), np.int32),
                    np.arange(n, dtype=np.int32)[:, None], np.ones(n, np.int32), pool, status=status)
     eng.close()
+
+
+def test_fp32_group_over_wide_table(tiny, cuda):
+    """The fp32 check mode runs every group on the per-token wave kernel,
+    which takes any block-table width: a group of 17 children over a
+    600-block table row is accepted and matches a full recompute."""
+    cfg, sd = tiny
+    rng = np.random.default_rng(17)
+    P, n = 40, 17
+    prefix = rng.integers(0, 1968, P)
+    eng = Engine(cfg, sd, mode="float32")
+    pool = nan_pool(eng, 8)
+    table = np.zeros((1, 600), np.int32)
+    table[0, :3] = [0, 1, 2]
+    eng.prefill(np.asarray(prefix, np.uint32), [P], kv_pool=pool,
+                kv_block_table=torch.from_numpy(table).to(cuda))
+    kids = rng.integers(0, 1968, n)
+    status = torch.full((1,), -1, dtype=torch.int32, device=cuda)
+    out = eng.extend(kids, np.full(n, P, np.int32), [n], [P], table, (3 * 16 + np.arange(n, dtype=np.int32))[:, None],
+                     np.ones(n, np.int32), pool, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    paths = [np.concatenate([prefix, [k]]).astype(np.int64) for k in kids]
+    check(out, RefModel(cfg, sd, mode="float32").forward_last(paths), 1e-4, "fp32 wide table")
+    eng.close()

@@ -5,9 +5,13 @@
   ``softmax(logits[:1968] / T).argmax()`` (src/evaluation/decode.py:223-226)
   and the legal move as ``softmax(legal logits / T).argmax()``
   (decode.py:112, 231): one NaN turns the whole softmax NaN and torch's
-  argmax then returns the first element.  The heads kernel must give the
-  same top-1, with max_logit and lse NaN, and the usual answer when the NaN
-  move is masked out.
+  argmax then returns the first element.  Over all moves the first element
+  is move id 0, so the heads kernel must give the reference's top-1 there,
+  with max_logit and lse NaN, and the usual answer when the NaN move is
+  masked out.  With a legal mask that keeps the NaN move, the reference's
+  first element is legal_moves[0] in python-chess generation order, which
+  is not available here (parity unpinned); the heads kernel follows a
+  stated convention instead: the smallest legal move id.
 * A KV pool too small for the prefill is rejected before any launch.
 * The packer's flags reach the caller through ``status``: the <PAD> id
   inside a game (8; the reference's padded batch would mask that token,
@@ -71,7 +75,8 @@ def test_nan_logit_follows_torch_softmax_argmax(tiny, mode, cuda):
         srt = sorted(ids)
         want = srt[int(torch.softmax(lg[b, srt] / T, dim=0).argmax())]
         assert int(r2.top1[b]) == want and np.isfinite(float(r2.lse[b]))
-    # legal moves including it: the first legal id (element 0 of the NaN softmax over the ids in order)
+    # legal moves including it: the smallest legal id (this library's convention; the reference's pick,
+    # legal_moves[0] in python-chess order, is unpinned)
     legal_nan = [[3, NAN_ID, 9], [NAN_ID, 700], [NAN_ID], [2, 4, NAN_ID], [6, NAN_ID, 1000], [NAN_ID, 1967]]
     r3 = eng.prefill(words, lens, temperature=T, legal=legal_mask(legal_nan))
     for b, ids in enumerate(legal_nan):

@@ -68,8 +68,8 @@ def test_continuous_batching_greedy_moves(tiny, mode, margin, cuda):
     torch.cuda.synchronize()
     assert int(cb.status.item()) == 0
     assert cb.games_started > 5  # slots were evicted and refilled
-    seqs = [np.asarray(g, np.int64) for g, _ in cb.checks]
-    pred = np.array([p for _, p in cb.checks])
+    seqs = [np.asarray(c.ids, np.int64) for c in cb.checks]
+    pred = np.array([c.move for c in cb.checks])
     assert max(len(g) for g in seqs) <= 64
     ref = RefModel(cfg, sd, mode=mode).forward_last(seqs)
     ps = policy_summary(ref["logits"])

@@ -3,9 +3,12 @@
 The allocation-free entry point runs the same kernels over the library's
 per-device scratch instead of a caller workspace, so its outputs must equal
 allie_extend's bit for bit.  Two calls in a row, the second smaller (the
-scratch keeps the first call's contents), on the tiny model (fan-kernel
-groups, then one-token decode groups) and on the medium model at the
-256-token maximum; one token more is rejected before any launch.
+scratch keeps the first call's contents), on the tiny model in each mode
+(bf16: fan-kernel groups, then one-token decode groups; fp8 weights, whose
+GEMMs widen the e4m3 bytes in registers here instead of in the workspace;
+the fp32 check mode), on the medium model at the 256-token maximum (one
+token more is rejected before any launch), and on the 2x fp8 shape at the
+maximum, which must fit the scratch.
 """
 import numpy as np
 import pytest
@@ -58,9 +61,10 @@ def run_both(eng, pool, b):
     return got
 
 
-def test_noalloc_equals_extend_tiny(cuda):
+@pytest.mark.parametrize("mode", ["bfloat16", "fp8w", "float32"])
+def test_noalloc_equals_extend_tiny(mode, cuda):
     cfg = config.TINY
-    eng = Engine(cfg, weights.init_weights(cfg, seed=5, perturb=True), mode="bfloat16")
+    eng = Engine(cfg, weights.init_weights(cfg, seed=5, perturb=True), mode=mode)
     pool, table, free = roots(eng, 4, 37, seed=1)
     rng = np.random.default_rng(2)
     slot0 = free * 16
@@ -87,4 +91,17 @@ def test_noalloc_medium_max_tokens(cuda):
     b3 = batch(rng, table, 200, [g % 4 for g in range(257)], 1, 1, slot0)  # one token over the maximum
     with pytest.raises(capi.AllieError, match="max 256"):
         eng.extend(**b3, kv_pool=pool, noalloc=True)
+    eng.close()
+
+
+def test_noalloc_2x_fp8_max_tokens(cuda):
+    cfg = config.LARGE2X
+    eng = Engine(cfg, weights.init_weights(cfg, seed=0), mode="fp8w")
+    pool, table, free = roots(eng, 4, 200, seed=3)
+    rng = np.random.default_rng(6)
+    slot0 = free * 16
+    b1 = batch(rng, table, 200, [g % 4 for g in range(16)], 16, 1, slot0)  # 256 tokens
+    run_both(eng, pool, b1)
+    b2 = batch(rng, table, 200, [1, 3], 1, 2, slot0 + 300)
+    run_both(eng, pool, b2)
     eng.close()
