@@ -65,6 +65,22 @@ def alg_flops(cfg, lens):
     return 2 * P * T + attn + heads
 
 
+def executed_flops(cfg, lens):
+    """FLOPs the prefill executes: the algorithmic count less what the last
+    block skips -- its attention c_proj and MLP run on each game's last row
+    only, and its attention on the 32-query tile holding that row (when
+    2 B <= T, as in C2)."""
+    lens = np.minimum(np.asarray(lens, np.int64), cfg.max_length)
+    T, B, d = int(lens.sum()), len(lens), cfg.d_model
+    full = alg_flops(cfg, lens)
+    if 2 * B > T:
+        return full
+    gemm_skip = 2 * (T - B) * (d * d + 2 * d * cfg.d_ff)
+    last_tile = lambda n: sum(range(32 * ((n - 1) // 32) + 1, n + 1))  # key counts of the tile's queries
+    attn_skip = 4 * d * int(sum(n * (n + 1) // 2 - last_tile(int(n)) for n in lens))
+    return full - gemm_skip - attn_skip
+
+
 def read_traffic(key: str = ""):
     """HBM bytes per launch of a dominant kernel, measured with rocprofv3
     --pmc FETCH_SIZE / WRITE_SIZE and scaled by the copy calibration: the
@@ -79,6 +95,19 @@ def read_traffic(key: str = ""):
         for line in f:
             if line.startswith(tag):
                 return float(line.split(":", 1)[1])
+    return None
+
+
+def traffic_commit(key: str = "") -> str | None:
+    """The kernel source and commit the traffic summary was measured on (its
+    ``kernel_commit:`` line), printed next to ``traffic``."""
+    path = TRAFFIC_FILE if not key else ATTN_TRAFFIC_FILE
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("kernel_commit:"):
+                return line.split(":", 1)[1].strip()
     return None
 
 
@@ -251,7 +280,10 @@ def run_prefill(args, cfg, mode, workload):
                       "bf16" if mode == "bfloat16" else "fp8 e4m3 weights, bf16 activations", workload,
                       n_seq=len(lens), n_tokens=T, tokens_per_s=T / (ms / 1000.0),
                       alg_tflop_per_step=flops / 1e12,
-                      whole_forward_mfma_frac=flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS)
+                      whole_forward_mfma_frac=flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+                      executed_tflop_per_step=executed_flops(cfg, lens) / 1e12,
+                      whole_forward_mfma_frac_executed=executed_flops(cfg, lens) / (ms * 1e-3) / 1e12
+                      / MFMA_BF16_PEAK_TFLOPS)
     res["roofline"] = {
         "kernel": ("gemm_big_kernel<EPI_GELU> (MLP c_fc, persistent 256x256 tiles)" if mode == "bfloat16"
                    else "widen_fp8_kernel + gemm_big_kernel<EPI_GELU,SCALED> (MLP c_fc, fp8 weights "
@@ -259,6 +291,7 @@ def run_prefill(args, cfg, mode, workload):
         "bound": "mfma", "achieved": fc_tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
         "frac": fc_tflops / MFMA_BF16_PEAK_TFLOPS,
         "traffic": read_traffic() if (mode == "bfloat16" and cfg.d_model == 1024) else None,
+        "traffic_measured_on": traffic_commit() if (mode == "bfloat16" and cfg.d_model == 1024) else None,
         "avg_launch_ms": fc_ms, "launches": fc_n,
         "alg_flop_per_launch": fc_flops,
     }
@@ -341,18 +374,24 @@ def bench_c3(args):
     level_ms = np.zeros(lay.depth)
     attn = {}
     for _ in range(args.steps):
-        t, attn = run_tree(probe_levels=(1, 2))
+        t, attn = run_tree(probe_levels=(1, 2, 4))
         level_ms += np.array(t)
     level_ms /= args.steps
     d, L, P = cfg.d_model, cfg.n_layer, lay.prefix_len
     kv_tok = 2 * d * 2  # bytes of one token's keys + values, one layer
     roof = {}
-    for k in (1, 2):
+    for k in (1, 2, 4):
         n = lay.level_size(k)
         bytes_ = lay.n_roots * P * kv_tok + n * k * kv_tok + n * 2 * d * 2
         tot, cnt = attn[k]
         ms = tot / max(cnt, 1)
         roof[k] = {"avg_launch_ms": ms, "alg_bytes_per_launch": bytes_, "achieved_GBs": bytes_ / (ms * 1e-3) / 1e9}
+    # level 4: every pool row once (ancestors shared by siblings), and its MFMA work
+    n4 = lay.level_size(4)
+    uniq = lay.n_roots * P * kv_tok + sum(lay.level_size(j) for j in range(1, 5)) * kv_tok + n4 * 2 * d * 2
+    fl4 = 4 * d * n4 * (P + 4)  # QK^T and PV over each node's P + 4 keys
+    roof[4].update(unique_bytes_per_launch=uniq, achieved_unique_GBs=uniq / (roof[4]["avg_launch_ms"] * 1e-3) / 1e9,
+                   alg_flop_per_launch=fl4, achieved_TFLOPs=fl4 / (roof[4]["avg_launch_ms"] * 1e-3) / 1e12)
     total_ms = float(level_ms.sum())
     leaves = lay.level_size(lay.depth)
     flops = sum(2 * cfg.linear_params * lay.level_size(k) + 4 * d * L * lay.level_size(k) * (P + k)
@@ -369,7 +408,9 @@ def bench_c3(args):
                                  "prefixes; level2: attn_extend_tree_kernel)",
                        "bound": "hbm", "achieved": a1["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": a1["achieved_GBs"] / HBM_PEAK_GBS, "traffic": read_traffic("c3_level1"),
-                       "level2": dict(roof[2], traffic=read_traffic("c3_level2"))}
+                       "traffic_measured_on": traffic_commit("c3_level1"),
+                       "level2": dict(roof[2], traffic=read_traffic("c3_level2")),
+                       "level4": dict(roof[4], traffic=read_traffic("c3_level4"))}
     eng.close()
     res["cpu_baseline"] = None
     if not args.no_cpu_baseline:
@@ -435,7 +476,8 @@ def bench_c4(args):
                       moves_appended=appended, games_started=cb.games_started)
     res["roofline"] = {"kernel": "attn_extend_wave_kernel (decode: one token per running game over its paged KV)",
                        "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                       "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic("c4_decode"), "avg_launch_ms": att_ms,
+                       "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic("c4_decode"),
+                       "traffic_measured_on": traffic_commit("c4_decode"), "avg_launch_ms": att_ms,
                        "alg_bytes_per_launch": att_bytes}
     eng.close()
     res["cpu_baseline"] = None
