@@ -241,7 +241,7 @@ def kl_regularised_policy(priors: torch.Tensor, values: torch.Tensor, visit_coun
 class MCTS(Policy):
     def init(self, n_sims: int = 50, depth_limit: int = 100, c_puct: float = 1.25, c_base: float = 19652.0,
              dummy_value_function: bool = False, kl_reg_solution: bool = True, kv_cache: bool = False,
-             leaf_batch: int = 1, **kwargs) -> None:
+             leaf_batch: int = 1, kv_graph: bool = True, **kwargs) -> None:
         super().init(**kwargs)
         self.n_sims = n_sims
         self.depth_limit = depth_limit
@@ -250,21 +250,24 @@ class MCTS(Policy):
         self.dummy_value_function = dummy_value_function
         self.kl_reg_solution = kl_reg_solution
         self.total_rollouts = 0
-        self._init_kv(kv_cache, leaf_batch)
+        self._init_kv(kv_cache, leaf_batch, kv_graph)
 
-    def _init_kv(self, kv_cache: bool, leaf_batch: int) -> None:
+    def _init_kv(self, kv_cache: bool, leaf_batch: int, kv_graph: bool = True) -> None:
         """Opt-in search over a paged KV cache (``allie_amd.search_kv``):
         ``kv_cache=True`` evaluates each leaf as one new token over its
         root's and ancestors' cached keys, with the reference's sequential
         semantics; ``leaf_batch=B > 1`` also selects up to B leaves per round
         under virtual loss and evaluates them in one call (a different,
-        batched search).  Neither exists in the reference."""
+        batched search); ``kv_graph`` (default on) replays single leaves from
+        a captured HIP graph, with identical results.  None of these exists
+        in the reference."""
         if leaf_batch < 1:
             raise ValueError("leaf_batch must be >= 1")
         if leaf_batch > 1 and not kv_cache:
             raise ValueError("leaf_batch > 1 needs kv_cache=True")
         self.kv_cache = kv_cache
         self.leaf_batch = leaf_batch
+        self.kv_graph = kv_graph
         self._kv: Optional[KVSearchCache] = None
 
     def check(self) -> None:
@@ -374,7 +377,7 @@ class MCTS(Policy):
         if not self.kv_cache:
             return None
         if self._kv is None:
-            self._kv = KVSearchCache(self.model.engine, self.tokenizer)
+            self._kv = KVSearchCache(self.model.engine, self.tokenizer, graph=self.kv_graph)
         return self._kv.begin(root, game, max_nodes)
 
     def _kv_end(self) -> None:
@@ -407,6 +410,7 @@ class MCTS(Policy):
         st = {"total_rollouts": self.total_rollouts}
         if self._kv is not None:
             st["kv_leaf_evaluations"] = self._kv.n_evals
+            st["kv_graph_replays"] = self._kv.n_graph
         return st
 
 
@@ -414,7 +418,7 @@ class AdaptiveMCTS(MCTS):
     def init(self, mean_n_sims: int = 50, depth_limit: int = 100, scale_c_puct: bool = True, c_puct: float = 1.25,
              c_base: float = 19652.0, dummy_value_function: bool = False, kl_reg_solution: bool = True,
              use_human_move_time: bool = False, conversion_strategy: str = "linear", kv_cache: bool = False,
-             leaf_batch: int = 1, **kwargs) -> None:
+             leaf_batch: int = 1, kv_graph: bool = True, **kwargs) -> None:
         Policy.init(self, **kwargs)
         self.mean_n_sims = mean_n_sims
         self.depth_limit = depth_limit
@@ -428,7 +432,7 @@ class AdaptiveMCTS(MCTS):
         assert conversion_strategy in ["linear", "binary"]
         self.conversion_strategy = conversion_strategy
         self.total_rollouts = 0
-        self._init_kv(kv_cache, leaf_batch)
+        self._init_kv(kv_cache, leaf_batch, kv_graph)
 
     def convert_time_to_sims(self, time_encoding: float) -> int:
         """decode.py:503-516."""

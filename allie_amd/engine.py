@@ -272,6 +272,24 @@ class Engine:
             capi.check(rc, "allie_extend")
         return out
 
+    def extend_noalloc_raw(self, ids, pos, group_start_host: np.ndarray, group_start, prefix_len, prefix_blocks,
+                           extra_slot, n_extra, kv_pool: torch.Tensor, out: PrefillResult,
+                           status: torch.Tensor, temperature: float = 1.0) -> None:
+        """``allie_extend_noalloc`` on device int32 tensors the caller owns
+        (``prefix_blocks`` [G, max_blocks], ``extra_slot`` [n, max_extra]) and
+        a preallocated ``out``: no tensor is created and nothing is copied, so
+        the call can be captured into a HIP graph and replayed with new
+        contents in the same buffers."""
+        G = len(group_start_host) - 1
+        n = int(group_start_host[-1])
+        o = _outputs(out)
+        rc = self._lib.allie_extend_noalloc(
+            self._m, capi.ptr(ids), capi.ptr(pos), n, group_start_host.ctypes.data_as(C.c_void_p),
+            capi.ptr(group_start), G, capi.ptr(prefix_len), capi.ptr(prefix_blocks), prefix_blocks.shape[1],
+            capi.ptr(extra_slot), capi.ptr(n_extra), extra_slot.shape[1], float(temperature), None, 0, C.byref(o),
+            capi.ptr(kv_pool), self.pool_blocks(kv_pool), capi.ptr(status), capi.stream_ptr())
+        capi.check(rc, "allie_extend_noalloc")
+
     def close(self) -> None:
         if getattr(self, "_m", None):
             self._lib.allie_model_destroy(self._m)

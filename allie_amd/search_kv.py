@@ -13,6 +13,15 @@ twice, :407 and :410).  Here one search keeps a paged KV pool:
   evaluated ancestors below the root and its own new slot, which receives its
   keys and values for its descendants.
 
+A single leaf (the sequential search's case) is evaluated by replaying a
+HIP graph of the allocation-free extend (``allie_extend_noalloc``) captured
+once per pool: its inputs -- the token, its position, its key count and
+pool slots, the root's prefix length and block table -- sit in one device
+buffer refreshed by one pinned copy, and its outputs come back in one copy.
+The graph runs the same kernels with the same arguments as the eager call,
+so its results are identical; it removes the per-kernel launch gaps and the
+host's argument staging (about 170 launches per leaf).
+
 The results equal the full recompute up to floating-point summation order:
 the same model, the same tokens, the same positions.  Where a node's game
 does not tokenize as its parent's tokens plus one move (a root with a result
@@ -40,11 +49,90 @@ class NodeEval:
     time: float
 
 
+class LeafGraph:
+    """One-token leaf evaluation over a search's pool, replayed from a HIP
+    graph.  Inputs live in one device int32 buffer ``[token, pos, n_keys,
+    prefix_len, 0, 1 (group starts), slots[MAX_EXTRA], table[max_blocks]]``;
+    outputs (logits, value, time, max logit, lse, top-1, status) in one fp32
+    buffer.  Captured for one pool; ``eligible`` says whether a leaf fits
+    (at most MAX_EXTRA private keys)."""
+
+    MAX_EXTRA = 64
+
+    def __init__(self, engine, pool: torch.Tensor, prefix_len: int, table: np.ndarray, slot: int):
+        from .engine import PrefillResult
+
+        self.eng, self.pool = engine, pool
+        dev = engine.device
+        V = engine.cfg.vocab_size
+        self.mb = (engine.cfg.max_length + KV_BLOCK - 1) // KV_BLOCK
+        E, MB = self.MAX_EXTRA, self.mb
+        self.n_in = 6 + E + MB
+        self.host = torch.zeros(self.n_in, dtype=torch.int32, pin_memory=True)
+        self.h = self.host.numpy()
+        self.inp = torch.zeros(self.n_in, dtype=torch.int32, device=dev)
+        self.gs_host = np.array([0, 1], np.int32)
+        self.outbuf = torch.zeros(V + 8, dtype=torch.float32, device=dev)
+        self.out_host = torch.zeros(V + 8, dtype=torch.float32, pin_memory=True)
+        ob = self.outbuf
+        self.out = PrefillResult(logits=ob[:V].view(1, V), value=ob[V:V + 1], time=ob[V + 1:V + 2],
+                                 top1=ob[V + 4:V + 5].view(torch.int32), max_logit=ob[V + 2:V + 3],
+                                 lse=ob[V + 3:V + 4])
+        self.status = ob[V + 5:V + 6].view(torch.int32)
+        self.V = V
+        # a valid leaf for the eager warm-up: the next free slot, overwritten by
+        # the first real leaf
+        self.set_root(prefix_len, table)
+        self._fill(0, prefix_len, [slot])
+        self.inp.copy_(self.host)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self._launch()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize(dev)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, capture_error_mode="thread_local"):
+            self._launch()
+
+    def _launch(self):
+        E, MB, i = self.MAX_EXTRA, self.mb, self.inp
+        self.eng.extend_noalloc_raw(i[0:1], i[1:2], self.gs_host, i[4:6], i[3:4], i[6 + E:6 + E + MB].view(1, MB),
+                                    i[6:6 + E].view(1, E), i[2:3], self.pool, self.out, self.status)
+
+    def set_root(self, prefix_len: int, table: np.ndarray) -> None:
+        E = self.MAX_EXTRA
+        self.h[3], self.h[4], self.h[5] = prefix_len, 0, 1
+        self.h[6 + E:] = 0
+        self.h[6 + E:6 + E + len(table)] = table
+
+    def _fill(self, token: int, pos: int, slots: list) -> None:
+        self.h[0], self.h[1], self.h[2] = token, pos, len(slots)
+        self.h[6:6 + len(slots)] = slots
+
+    def eligible(self, n_keys: int) -> bool:
+        return n_keys <= self.MAX_EXTRA
+
+    def run(self, token: int, pos: int, slots: list) -> "NodeEval":
+        self._fill(token, pos, slots)
+        self.inp.copy_(self.host, non_blocking=True)
+        self.graph.replay()
+        self.out_host.copy_(self.outbuf, non_blocking=True)
+        torch.cuda.current_stream().synchronize()
+        o = self.out_host
+        st = int(o[self.V + 5:self.V + 6].view(torch.int32).item())
+        if st != 0:
+            raise RuntimeError(f"KV search leaf rejected its inputs on the device (status {st})")
+        return NodeEval(o[:self.V].clone(), float(o[self.V]), float(o[self.V + 1]))
+
+
 class KVSearchCache:
     """Paged KV state of one search at a time on one engine.  The pool is
-    kept and reused across searches; it grows when a search needs more."""
+    kept and reused across searches; it grows when a search needs more.
+    ``graph`` (default on): single leaves replay a captured HIP graph
+    (``LeafGraph``); off, every leaf is an eager ``Engine.extend``."""
 
-    def __init__(self, engine, tokenizer):
+    def __init__(self, engine, tokenizer, graph: bool = True):
         self.eng = engine
         self.tok = tokenizer
         self.max_length = engine.cfg.max_length
@@ -52,6 +140,9 @@ class KVSearchCache:
         self.status: Optional[torch.Tensor] = None  # device int32 [1]: validation flags of the last call
         self.active = False
         self.n_evals = 0  # leaf evaluations made through extend (statistics)
+        self.use_graph = graph
+        self.leaf_graph: Optional[LeafGraph] = None
+        self.n_graph = 0  # of which replayed from the graph
 
     # ----------------------------------------------------------------- root
     def begin(self, root, game, max_nodes: int) -> Optional[NodeEval]:
@@ -71,6 +162,7 @@ class KVSearchCache:
         need = pb + (max_nodes + KV_BLOCK - 1) // KV_BLOCK
         if self.pool is None or self.eng.pool_blocks(self.pool) < need:
             self.pool = None
+            self.leaf_graph = None  # captured for the old pool
             self.pool = self.eng.new_kv_pool(need)
         self.n_slots = self.eng.pool_blocks(self.pool) * KV_BLOCK
         self.prefix_len = P
@@ -86,6 +178,12 @@ class KVSearchCache:
         root._kv_eval = ev
         self.root = root
         self.active = True
+        if self.use_graph:
+            table = np.arange(pb, dtype=np.int32)
+            if self.leaf_graph is None:
+                self.leaf_graph = LeafGraph(self.eng, self.pool, P, table, self.next_slot)
+            else:
+                self.leaf_graph.set_root(P, table)
         return ev
 
     def _check_status(self, what: str) -> None:
@@ -120,7 +218,18 @@ class KVSearchCache:
         """Evaluate nodes that ``can_extend`` in one extend call (one token
         each, all sharing the root's prefix); memoised nodes are not redone."""
         todo = [n for n in nodes if getattr(n, "_kv_eval", None) is None]
-        if todo:
+        lg = self.leaf_graph if self.use_graph else None
+        if len(todo) == 1 and lg is not None and lg.eligible(len(todo[0]._kv_parent._kv_path) + 1):
+            n = todo[0]
+            if self.next_slot + 1 > self.n_slots:
+                raise RuntimeError("KV search pool exhausted (more evaluations than the search was sized for)")
+            path = n._kv_parent._kv_path + [self.next_slot]
+            self.next_slot += 1
+            n._kv_eval = lg.run(n._kv_token, self.prefix_len + len(path) - 1, path)
+            n._kv_path = path
+            self.n_evals += 1
+            self.n_graph += 1
+        elif todo:
             if self.next_slot + len(todo) > self.n_slots:
                 raise RuntimeError("KV search pool exhausted (more evaluations than the search was sized for)")
             paths = []

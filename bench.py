@@ -520,7 +520,8 @@ def search_games(n_games: int, plies: int, seed: int = 11):
 def bench_search(args):
     """One MCTS decision (``score_full``, n_sims simulations) on the medium
     bf16 model: the reference's full recompute per leaf, the KV-cached
-    search (same sequential semantics), and KV with leaf batching."""
+    search (same sequential semantics; each leaf replayed from a captured
+    HIP graph, and launched eagerly), and KV with leaf batching."""
     import torch
 
     from allie_amd import config, weights
@@ -533,7 +534,8 @@ def bench_search(args):
     model = AllieModel.from_state_dict(cfg, weights.init_weights(cfg, seed=0), mode="bfloat16")
     tok = UCITokenizer(max_length=512)
     games = search_games(args.warmup + args.steps, plies=60)
-    modes = {"recompute": {}, "kv": {"kv_cache": True}, "kv_batch16": {"kv_cache": True, "leaf_batch": 16}}
+    modes = {"recompute": {}, "kv": {"kv_cache": True}, "kv_eager": {"kv_cache": True, "kv_graph": False},
+             "kv_batch16": {"kv_cache": True, "leaf_batch": 16}}
     ms = {}
     for name, kw in modes.items():
         strat = DECODE_STRATEGIES["mcts"](model, tok, device="cuda", precision="bfloat16", n_sims=n_sims, **kw)
@@ -552,8 +554,9 @@ def bench_search(args):
                       ms_per_decision={k: round(v, 2) for k, v in ms.items()},
                       sims_per_s={k: round(n_sims / (v / 1000.0), 1) for k, v in ms.items()},
                       speedup_kv_vs_recompute=ms["recompute"] / ms["kv"],
-                      note="kv_batch16 is a different (virtual-loss batched) search; recompute and kv make "
-                           "the same decisions")
+                      note="kv replays each leaf from a captured HIP graph, kv_eager launches it kernel by "
+                           "kernel; kv_batch16 is a different (virtual-loss batched) search; recompute, kv and "
+                           "kv_eager make the same decisions")
     res["metric"] = "MCTS simulations/s per decision (not a SURVEY headline metric)"
     res["roofline"] = None
     res["cpu_baseline"] = None

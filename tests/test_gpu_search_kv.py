@@ -158,3 +158,47 @@ def test_leaf_batching_bookkeeping(tiny):
     r = s.score_full(g, g.legal_moves)
     p = r.legal_move_probabilities
     assert torch.isfinite(p).all() and abs(float(p.sum()) - 1) < 1e-5
+
+
+@pytest.mark.parametrize("mode", ["float32", "bfloat16"])
+def test_leaf_graph_replays_equal_eager(cuda, mode):
+    """Single leaves replay a captured HIP graph of the allocation-free
+    extend.  Over two searches on one cache (the graph captured once, the
+    root's prefix length and table changed between them), every replay --
+    with eager extends and synchronisations in between -- equals the eager
+    allie_extend of the same leaf bit for bit, and the full forward of the
+    leaf's game within the mode's bar."""
+    cfg = config.TINY
+    sd = weights.init_weights(cfg, seed=21, perturb=True)
+    gpu = AllieModel.from_state_dict(cfg, sd, mode=mode)
+    tol = 1e-4 if mode == "float32" else 2e-2
+    try:
+        tok = UCITokenizer(max_length=512)
+        kv = KVSearchCache(gpu.engine, tok)
+        rng = np.random.default_rng(3)
+        for plies in (8, 13):
+            g = game(plies)
+            root = MCTSNode(0.0, g)
+            kv.begin(root, g, max_nodes=64)
+            graph = kv.leaf_graph
+            node = root
+            for depth in range(1, 7):
+                moves = node.game.legal_moves
+                m = moves[int(rng.integers(len(moves)))]
+                c = MCTSNode(0.0, node.game.make_move(m))
+                kv.attach(node, c, m)
+                before = kv.n_graph
+                ev = kv.evaluate([c])[0]
+                assert kv.n_graph == before + 1 and kv.leaf_graph is graph
+                path = c._kv_path
+                eager = gpu.engine.extend([c._kv_token], [kv.prefix_len + len(path) - 1], [1], [kv.prefix_len],
+                                          kv.table, np.asarray(path, np.int32)[None], [len(path)], kv.pool)
+                assert torch.equal(ev.logits, eager.logits[0].cpu()), (mode, plies, depth)
+                assert ev.value == float(eager.value[0]) and ev.time == float(eager.time[0])
+                ref = full_eval(gpu, tok, c.game)
+                assert np.abs(ev.logits.numpy() - ref[0]).max() <= tol
+                assert abs(ev.value - ref[1]) <= tol and abs(ev.time - ref[2]) <= tol
+                node = c
+            kv.end()
+    finally:
+        gpu.close()
