@@ -228,7 +228,8 @@ def test_c5_fp8_weights_at_size(cuda):
     ps = policy_summary(b["logits"])
     agree = all_fp8["top1"] == b["top1"]
     clear = ps["margin"] > 2 * err
-    print(f"c5 quality: top-1 agreement with bf16 {agree.mean():.3f} over 256 games; "
+    print(f"c5 quality: raw top-1 agreement with bf16 {agree.mean():.3f} over 256 games (the ablation's bar "
+          f">= 0.99 is {'met' if agree.mean() >= 0.99 else 'not met on these random-init weights'}); beside it "
           f"{agree[clear].mean() if clear.any() else float('nan'):.3f} over the {int(clear.sum())} games whose "
           f"bf16 top-2 margin exceeds twice their fp8 logit error; max |dlogit| {err.max():.3f}", flush=True)
     assert agree[clear].all()
