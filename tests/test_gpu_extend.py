@@ -110,8 +110,9 @@ def test_decode_long_games(tiny, cuda):
 # prefix tables of at most 8 chunks take the split-prefix kernels in bf16
 # (level 1 of the second case: full, ragged and one-block prefixes, a group of
 # one child after the others), and level 2 of that case (groups of up to 32)
-# the tree kernel again
-TREES = [([37, 64, 100], [3, 70, 5]), ([37, 64, 100, 128, 5], [3, 16, 5, 1, 9])]
+# the tree kernel again; in the third case level 2 holds a group of 300 tokens
+# (more than one 256-query tile), which takes the span kernel in bf16
+TREES = [([37, 64, 100], [3, 70, 5]), ([37, 64, 100, 128, 5], [3, 16, 5, 1, 9]), ([37, 100], [150, 9])]
 
 
 @pytest.mark.parametrize("prefix,kids", TREES)
