@@ -879,8 +879,11 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmArgs a) {
     for (; kt < KT; ++kt) k_tile(cur, kt, 0, std::false_type{});
 
     // KV: a tile of key / value columns goes to the pool, row by row at the
-    // rows' slots; the slots of this lane's 16 rows load before the next
-    // tile's head, so waiting for them does not wait for that
+    // rows' slots.  The slots of this lane's 16 rows load here: without early
+    // refill that is before the next tile's head (issued below), so waiting
+    // for them does not wait for it; with early refill the head went out in
+    // the last two k-tiles, and since loads complete in order the wait for
+    // the slots also waits for it (time only, at the KV tiles of a QKV GEMM)
     const int d3 = a.N / 3;
     const bool kv_tile = KV && cur.n0 + big::BN > d3;
     int slot[FM][4];
