@@ -77,6 +77,7 @@ _SIGS = [
       C.c_float, C.c_void_p, C.c_int, C.POINTER(AllieOutputs),  # temperature, legal, words, out
       C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]),          # kv_pool, pool blocks, status, stream
     ("allie_probe_begin", C.c_int, [C.c_int, C.c_int]),
+    ("allie_probe_span", C.c_int, [C.POINTER(C.c_float)]),
     ("allie_probe_end", C.c_int, [C.POINTER(C.c_float), C.POINTER(C.c_int)]),
     ("allie_gemm", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int,

@@ -5,6 +5,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -140,6 +141,10 @@ struct allie_model {
   std::vector<LayerW> layers;
   std::vector<uint8_t> set;  // [(L + 1) * N_KINDS]
   bool ready = false;
+  // a large prefill runs as two halves on these streams (default priority),
+  // forked from and joined back into the caller's stream by the events
+  hipStream_t side[2] = {nullptr, nullptr};
+  hipEvent_t fork = nullptr, join[2] = {nullptr, nullptr};
 };
 
 namespace {
@@ -584,6 +589,120 @@ ExtendWS layout_extend(const allie_model* m, int n, int G, char* base, bool with
   return w;
 }
 
+// A bf16 prefill of at least this many tokens (and no KV pool or status
+// output) runs as two halves on two streams
+constexpr int64_t PREFILL_SPLIT_TOKENS = 24576;
+
+// One prefill forward of n_seq games (T tokens) over the laid-out workspace
+// w, on stream st (arguments checked by allie_prefill).
+int prefill_batch(allie_model* m, const uint32_t* words, const int32_t* lens_host, int n_seq, int64_t T,
+                  float temperature, const uint32_t* legal, int legal_words, const allie_outputs* out,
+                  void* kv_pool, int kv_pool_blocks, int first_block, const int32_t* kv_block_table,
+                  int kv_max_blocks, int32_t* status, const PrefillWS& w, hipStream_t st) {
+  int rc;
+  const int d = m->d, L = m->L, act = m->act_bf16;
+  const int max_len = m->cfg.max_length;
+  int64_t n_tiles = 0;
+  for (int i = 0; i < n_seq; ++i) {
+    const int n = lens_host[i] < max_len ? lens_host[i] : max_len;
+    n_tiles += (n + ATTN_Q_TILE - 1) / ATTN_Q_TILE;
+  }
+  const float eps = m->cfg.eps;
+
+  if ((rc = upload_i32(m, w.lens, lens_host, (size_t)n_seq, st))) return rc;
+  PackArgs p{};
+  p.words = words;
+  p.lens = w.lens;
+  p.B = n_seq;
+  p.max_len = max_len;
+  p.block = KV_BLOCK;
+  p.first_block = first_block;
+  p.max_blocks = (max_len + KV_BLOCK - 1) / KV_BLOCK;
+  p.q_tile = ATTN_Q_TILE;
+  p.capacity = (int)T;
+  p.cu_seqlens = w.cu;
+  p.in_off = w.in_off;
+  p.ids = w.ids;
+  p.pos = w.pos;
+  p.seq_of = w.seq_of;
+  p.last_idx = w.last;
+  p.blk_off = w.blk_off;
+  p.block_table = nullptr;
+  p.slot = kv_pool ? w.slot : nullptr;
+  p.tiles = w.tiles;
+  p.block_table_in = kv_block_table;
+  p.max_blocks_in = kv_max_blocks;
+  p.pad_id = ALLIE_PAD_ID;
+  p.status = status ? status : w.status;
+  HIP_TRY(launch_pack(p, st));
+
+  EmbedArgs ea{};
+  ea.ids = w.ids;
+  ea.pos = w.pos;
+  ea.T = (int)T;
+  ea.d = d;
+  ea.vocab = m->V;
+  ea.n_positions = m->cfg.n_positions;
+  ea.wte = m->wte;
+  ea.wpe = m->wpe;
+  ea.ctrl = m->ctrl;
+  ea.ln_g = m->layers[0].ln1_g;
+  ea.ln_b = m->layers[0].ln1_b;
+  ea.eps = eps;
+  ea.h = w.h;
+  ea.x = w.x;
+  ea.act_bf16 = act;
+  HIP_TRY(launch_embed_ln(ea, st));
+
+  AttnVarlenArgs aa{};
+  aa.qkv = w.qkv;
+  aa.cu_seqlens = w.cu;
+  aa.tiles = w.tiles;
+  aa.n_tiles = (int)n_tiles;
+  aa.order = w.order;
+  aa.B = n_seq;
+  aa.T = (int)T;
+  aa.n_head = m->H;
+  aa.head_dim = m->hd;
+  aa.scale = 0.125f;  // 1 / sqrt(64)
+  aa.out = w.attn;
+  aa.act_bf16 = act;
+
+  const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff, w.part, w.wdq};
+  // Only each game's last token reaches the heads, so the last block's c_proj,
+  // ln_2 and MLP run on those n_seq rows (when they are at most half the
+  // tokens): its attention output and residual rows are gathered into x
+  // (free once the block's QKV has read it) and ff (not yet written).
+  Compact cp{};
+  const bool compact = 2 * (int64_t)n_seq <= T;
+  if (compact) {
+    const size_t a = act ? 2 : 4;
+    cp.idx = w.last;
+    cp.n = n_seq;
+    cp.attn = w.x;
+    cp.x = (char*)w.x + align_up((size_t)n_seq * d * a);
+    cp.h = (float*)w.ff;
+    cp.ff = (char*)w.ff + align_up((size_t)n_seq * d * 4);
+  }
+  const void* final_add = nullptr;
+  const float* h_final = nullptr;
+  rc = run_layers(m, acts, (int)T, kv_pool ? w.slot : nullptr, kv_pool, kv_pool_blocks, false,
+                  [&](int layer) -> int {
+                    HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, true, st));
+                    aa.order_ready = layer > 0;  // the game order is computed once per forward
+                    aa.last_only = compact && layer == L - 1;  // only the compact rows are read
+                    HIP_TRY(launch_attn_varlen(aa, st));
+                    HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, false, st));
+                    return ALLIE_OK;
+                  },
+                  st, compact ? &cp : nullptr, &h_final, &final_add);
+  if (rc) return rc;
+  // heads on the last token of every game (row b of the compact rows is game b's)
+  return run_heads(m, h_final, final_add, compact ? nullptr : w.last, n_seq, w.hx, w.z, temperature, legal,
+                   legal_words, out, w.part, st);
+}
+
+
 }  // namespace
 
 extern "C" {
@@ -638,12 +757,32 @@ int allie_model_create(const allie_config* cfg, allie_model** out) {
     return fail(ALLIE_ERR_HIP, "hipMemset: %s", hipGetErrorString(e));
   }
   m->set.assign((size_t)(m->L + 1) * N_KINDS, 0);
+  // the two streams of a split prefill and their fork / join events
+  if (m->act_bf16) {
+    for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+      e = hipStreamCreateWithFlags(&m->side[i], hipStreamNonBlocking);
+      if (e == hipSuccess) e = hipEventCreateWithFlags(&m->join[i], hipEventDisableTiming);
+    }
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&m->fork, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      allie_model_destroy(m);
+      return fail(ALLIE_ERR_HIP, "stream / event creation: %s", hipGetErrorString(e));
+    }
+  }
   *out = m;
   return ALLIE_OK;
 }
 
 void allie_model_destroy(allie_model* m) {
   if (!m) return;
+  for (int i = 0; i < 2; ++i) {
+    if (m->side[i]) {
+      hipStreamSynchronize(m->side[i]);
+      hipStreamDestroy(m->side[i]);
+    }
+    if (m->join[i]) hipEventDestroy(m->join[i]);
+  }
+  if (m->fork) hipEventDestroy(m->fork);
   for (int i = 0; i < PinnedRing::N; ++i) {
     if (m->pinned.ev[i]) {
       hipEventSynchronize(m->pinned.ev[i]);
@@ -820,7 +959,13 @@ int allie_pack_ragged(const uint32_t* words, const int32_t* lens, int n_seq, int
 
 size_t allie_prefill_workspace_bytes(const allie_model* m, int n_seq, int n_tokens) {
   if (!m || n_seq < 0 || n_tokens < 0) return 0;
-  return layout_prefill(m, n_seq, n_tokens, nullptr).total;
+  size_t b = layout_prefill(m, n_seq, n_tokens, nullptr).total;
+  // a prefill that runs as two halves needs a second copy of the per-game
+  // and fixed parts and the alignment of the second half's arrays (a smaller
+  // workspace runs it in one piece)
+  if (m->act_bf16 && n_tokens >= PREFILL_SPLIT_TOKENS && n_seq >= 2)
+    b += layout_prefill(m, n_seq, 0, nullptr).total + 32 * 256;
+  return b;
 }
 
 size_t allie_kv_block_bytes(const allie_model* m) {
@@ -841,12 +986,11 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
     return fail(ALLIE_ERR_ARG, "value/time/top1/max_logit/lse outputs are required");
   if (legal && legal_words * 32 < 1968) return fail(ALLIE_ERR_ARG, "legal mask too narrow");
   const int max_len = m->cfg.max_length;
-  int64_t T = 0, n_tiles = 0, n_blocks = 0;
+  int64_t T = 0, n_blocks = 0;
   for (int i = 0; i < n_seq; ++i) {
     if (lens_host[i] <= 0) return fail(ALLIE_ERR_LENGTH, "game %d is empty", i);
     const int n = lens_host[i] < max_len ? lens_host[i] : max_len;
     T += n;
-    n_tiles += (n + ATTN_Q_TILE - 1) / ATTN_Q_TILE;
     n_blocks += (n + KV_BLOCK - 1) / KV_BLOCK;
   }
   if (T > (int64_t)1 << 30) return fail(ALLIE_ERR_ARG, "too many tokens");
@@ -854,104 +998,67 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
   if (kv_pool && !kv_block_table && (first_block < 0 || first_block + n_blocks > kv_pool_blocks))
     return fail(ALLIE_ERR_LENGTH, "KV pool too small: need blocks [%d, %lld), have %d", first_block,
                 (long long)(first_block + n_blocks), kv_pool_blocks);
-  PrefillWS w = layout_prefill(m, n_seq, (int)T, (char*)workspace);
+  hipStream_t st = (hipStream_t)stream;
+  const PrefillWS w = layout_prefill(m, n_seq, (int)T, (char*)workspace);
+  // Large bf16 batches run as two halves of consecutive games, one per side
+  // stream: the halves' kernels fill each other's idle resources (a
+  // LayerNorm or attention of one half beside the other's persistent GEMM,
+  // the GEMMs' last partial rounds).  Rows never interact across games, so
+  // each half computes exactly what the whole batch would for its games.
+  int cut = 0;
+  int64_t T0 = 0;
+  if (m->act_bf16 && !kv_pool && !status && T >= PREFILL_SPLIT_TOKENS && n_seq >= 2) {
+    int64_t acc = 0;
+    for (int i = 0; i < n_seq - 1; ++i) {
+      acc += lens_host[i] < max_len ? lens_host[i] : max_len;
+      if (2 * acc >= T) {
+        cut = i + 1;
+        T0 = acc;
+        break;
+      }
+    }
+    if (cut == 0) {
+      cut = n_seq - 1;
+      T0 = acc;
+    }
+  }
+  if (cut > 0) {
+    const PrefillWS w0 = layout_prefill(m, cut, (int)T0, (char*)workspace);
+    const PrefillWS w1 = layout_prefill(m, n_seq - cut, (int)(T - T0), (char*)workspace + w0.total);
+    int dev = -1;
+    if (w0.total + w1.total > workspace_bytes || !m->fork || hipGetDevice(&dev) != hipSuccess || dev != m->device)
+      cut = 0;
+    if (cut > 0) {
+      HIP_TRY(hipEventRecord(m->fork, st));
+      int64_t words0 = 0;  // the second half's words start after the first half's games
+      for (int i = 0; i < cut; ++i) words0 += lens_host[i];
+      allie_outputs o1 = *out;
+      auto shift = [&](auto* p, int64_t n) { return p ? p + n : p; };
+      o1.logits = shift(out->logits, (int64_t)cut * m->V);
+      o1.logits_raw = shift(out->logits_raw, (int64_t)cut * m->V);
+      o1.value = out->value + cut;
+      o1.time = out->time + cut;
+      o1.top1 = out->top1 + cut;
+      o1.max_logit = out->max_logit + cut;
+      o1.lse = out->lse + cut;
+      for (int i = 0; i < 2; ++i) {
+        HIP_TRY(hipStreamWaitEvent(m->side[i], m->fork, 0));
+        rc = i == 0 ? prefill_batch(m, words, lens_host, cut, T0, temperature, legal, legal_words, out, nullptr, 0,
+                                    0, nullptr, 0, nullptr, w0, m->side[0])
+                    : prefill_batch(m, words + words0, lens_host + cut, n_seq - cut, T - T0, temperature,
+                                    legal ? legal + (int64_t)cut * legal_words : nullptr, legal_words, &o1, nullptr,
+                                    0, 0, nullptr, 0, nullptr, w1, m->side[1]);
+        if (rc) return rc;
+        HIP_TRY(hipEventRecord(m->join[i], m->side[i]));
+        HIP_TRY(hipStreamWaitEvent(st, m->join[i], 0));
+      }
+      return ALLIE_OK;
+    }
+  }
   if (workspace_bytes < w.total)
     return fail(ALLIE_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, w.total);
-  hipStream_t st = (hipStream_t)stream;
-  const int d = m->d, L = m->L, act = m->act_bf16;
-  const float eps = m->cfg.eps;
-
-  if ((rc = upload_i32(m, w.lens, lens_host, (size_t)n_seq, st))) return rc;
-  PackArgs p{};
-  p.words = words;
-  p.lens = w.lens;
-  p.B = n_seq;
-  p.max_len = max_len;
-  p.block = KV_BLOCK;
-  p.first_block = first_block;
-  p.max_blocks = (max_len + KV_BLOCK - 1) / KV_BLOCK;
-  p.q_tile = ATTN_Q_TILE;
-  p.capacity = (int)T;
-  p.cu_seqlens = w.cu;
-  p.in_off = w.in_off;
-  p.ids = w.ids;
-  p.pos = w.pos;
-  p.seq_of = w.seq_of;
-  p.last_idx = w.last;
-  p.blk_off = w.blk_off;
-  p.block_table = nullptr;
-  p.slot = kv_pool ? w.slot : nullptr;
-  p.tiles = w.tiles;
-  p.block_table_in = kv_block_table;
-  p.max_blocks_in = kv_max_blocks;
-  p.pad_id = ALLIE_PAD_ID;
-  p.status = status ? status : w.status;
-  HIP_TRY(launch_pack(p, st));
-
-  EmbedArgs ea{};
-  ea.ids = w.ids;
-  ea.pos = w.pos;
-  ea.T = (int)T;
-  ea.d = d;
-  ea.vocab = m->V;
-  ea.n_positions = m->cfg.n_positions;
-  ea.wte = m->wte;
-  ea.wpe = m->wpe;
-  ea.ctrl = m->ctrl;
-  ea.ln_g = m->layers[0].ln1_g;
-  ea.ln_b = m->layers[0].ln1_b;
-  ea.eps = eps;
-  ea.h = w.h;
-  ea.x = w.x;
-  ea.act_bf16 = act;
-  HIP_TRY(launch_embed_ln(ea, st));
-
-  AttnVarlenArgs aa{};
-  aa.qkv = w.qkv;
-  aa.cu_seqlens = w.cu;
-  aa.tiles = w.tiles;
-  aa.n_tiles = (int)n_tiles;
-  aa.order = w.order;
-  aa.B = n_seq;
-  aa.T = (int)T;
-  aa.n_head = m->H;
-  aa.head_dim = m->hd;
-  aa.scale = 0.125f;  // 1 / sqrt(64)
-  aa.out = w.attn;
-  aa.act_bf16 = act;
-
-  const Acts acts{w.h, w.x, w.qkv, w.attn, w.ff, w.part, w.wdq};
-  // Only each game's last token reaches the heads, so the last block's c_proj,
-  // ln_2 and MLP run on those n_seq rows (when they are at most half the
-  // tokens): its attention output and residual rows are gathered into x
-  // (free once the block's QKV has read it) and ff (not yet written).
-  Compact cp{};
-  const bool compact = 2 * (int64_t)n_seq <= T;
-  if (compact) {
-    const size_t a = act ? 2 : 4;
-    cp.idx = w.last;
-    cp.n = n_seq;
-    cp.attn = w.x;
-    cp.x = (char*)w.x + align_up((size_t)n_seq * d * a);
-    cp.h = (float*)w.ff;
-    cp.ff = (char*)w.ff + align_up((size_t)n_seq * d * 4);
-  }
-  const void* final_add = nullptr;
-  const float* h_final = nullptr;
-  rc = run_layers(m, acts, (int)T, kv_pool ? w.slot : nullptr, kv_pool, kv_pool_blocks, false,
-                  [&](int layer) -> int {
-                    HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, true, st));
-                    aa.order_ready = layer > 0;  // the game order is computed once per forward
-                    aa.last_only = compact && layer == L - 1;  // only the compact rows are read
-                    HIP_TRY(launch_attn_varlen(aa, st));
-                    HIP_TRY(probe_mark(ALLIE_PROBE_ATTN, false, st));
-                    return ALLIE_OK;
-                  },
-                  st, compact ? &cp : nullptr, &h_final, &final_add);
-  if (rc) return rc;
-  // heads on the last token of every game (row b of the compact rows is game b's)
-  return run_heads(m, h_final, final_add, compact ? nullptr : w.last, n_seq, w.hx, w.z, temperature, legal,
-                   legal_words, out, w.part, st);
+  return prefill_batch(m, words, lens_host, n_seq, T, temperature, legal, legal_words, out, kv_pool, kv_pool_blocks,
+                       first_block, kv_block_table, kv_max_blocks, status, w, st);
 }
 
 size_t allie_extend_workspace_bytes(const allie_model* m, int n_tok, int n_groups) {
@@ -1204,6 +1311,31 @@ int allie_probe_begin(int kind, int max_launches) {
     HIP_TRY(hipEventCreate(&g_probe.stop[i]));
   }
   g_probe.kind = kind;
+  return ALLIE_OK;
+}
+
+int allie_probe_span(float* span_ms_host) {
+  if (!span_ms_host) return fail(ALLIE_ERR_ARG, "NULL argument");
+  const int n = g_probe.n;
+  std::vector<std::pair<float, float>> iv((size_t)n);
+  for (int i = 0; i < n; ++i) {
+    HIP_TRY(hipEventSynchronize(g_probe.stop[i]));
+    HIP_TRY(hipEventElapsedTime(&iv[i].first, g_probe.start[0], g_probe.start[i]));
+    HIP_TRY(hipEventElapsedTime(&iv[i].second, g_probe.start[0], g_probe.stop[i]));
+  }
+  std::sort(iv.begin(), iv.end());
+  float span = 0.f, lo = 0.f, hi = 0.f;
+  for (int i = 0; i < n; ++i) {
+    if (i == 0 || iv[i].first > hi) {
+      span += hi - lo;
+      lo = iv[i].first;
+      hi = iv[i].second;
+    } else if (iv[i].second > hi) {
+      hi = iv[i].second;
+    }
+  }
+  if (n > 0) span += hi - lo;
+  *span_ms_host = span;
   return ALLIE_OK;
 }
 

@@ -19,10 +19,14 @@
 
 namespace {
 
+// Normalises the wave's register-resident row v and stores it as row `row`
+// of y.  Gamma and beta are loaded group by group after the statistics, so
+// the row costs few registers (an add + LayerNorm wave fits beside a
+// persistent GEMM wave on one SIMD: that GEMM leaves 48-56 of 512 free).
 template <int NV>
-__device__ __forceinline__ void ln_row_store_gb(const float4 (&v)[NV], int d, const float4 (&gg)[NV],
-                                                const float4 (&bb)[NV], float eps, void* y, int64_t row,
-                                                int act_bf16) {
+__device__ __forceinline__ void ln_row_store(const float4 (&v)[NV], int d, const float* __restrict__ g,
+                                             const float* __restrict__ b, float eps, void* y, int64_t row,
+                                             int act_bf16) {
   const int lane = threadIdx.x & 63;
   float s = 0.f;
 #pragma unroll
@@ -38,42 +42,21 @@ __device__ __forceinline__ void ln_row_store_gb(const float4 (&v)[NV], int d, co
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = (i * 64 + lane) * 4;
-    float o0 = (v[i].x - mean) * rstd * gg[i].x + bb[i].x;
-    float o1 = (v[i].y - mean) * rstd * gg[i].y + bb[i].y;
-    float o2 = (v[i].z - mean) * rstd * gg[i].z + bb[i].z;
-    float o3 = (v[i].w - mean) * rstd * gg[i].w + bb[i].w;
+    const float4 gg = *reinterpret_cast<const float4*>(g + c);
+    const float4 bb = *reinterpret_cast<const float4*>(b + c);
+    float o0 = (v[i].x - mean) * rstd * gg.x + bb.x;
+    float o1 = (v[i].y - mean) * rstd * gg.y + bb.y;
+    float o2 = (v[i].z - mean) * rstd * gg.z + bb.z;
+    float o3 = (v[i].w - mean) * rstd * gg.w + bb.w;
     if (act_bf16) {
       uint2 p;
       p.x = pack_bf16x2(o0, o1);
       p.y = pack_bf16x2(o2, o3);
       *reinterpret_cast<uint2*>(reinterpret_cast<bf16_t*>(y) + row * d + c) = p;
     } else {
-      *reinterpret_cast<float4*>(reinterpret_cast<float*>(y) + row * d + c) =
-          make_float4(o0, o1, o2, o3);
+      *reinterpret_cast<float4*>(reinterpret_cast<float*>(y) + row * d + c) = make_float4(o0, o1, o2, o3);
     }
   }
-}
-
-// this lane's gamma and beta (columns 4 (64 i + lane) .. +3)
-template <int NV>
-__device__ __forceinline__ void ln_load_gb(const float* __restrict__ g, const float* __restrict__ b,
-                                           float4 (&gg)[NV], float4 (&bb)[NV]) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    gg[i] = *reinterpret_cast<const float4*>(g + (i * 64 + lane) * 4);
-    bb[i] = *reinterpret_cast<const float4*>(b + (i * 64 + lane) * 4);
-  }
-}
-
-template <int NV>
-__device__ __forceinline__ void ln_row_store(const float4 (&v)[NV], int d,
-                                             const float* __restrict__ g,
-                                             const float* __restrict__ b, float eps, void* y,
-                                             int64_t row, int act_bf16) {
-  float4 gg[NV], bb[NV];
-  ln_load_gb<NV>(g, b, gg, bb);
-  ln_row_store_gb<NV>(v, d, gg, bb, eps, y, row, act_bf16);
 }
 
 template <int NV>
@@ -149,9 +132,8 @@ __global__ __launch_bounds__(256) void layernorm_kernel(allie::LNArgs a) {
     return;
   }
   const int64_t src = a.row_idx ? (int64_t)a.row_idx[r] : r;
-  float4 v[NV], gg[NV], bb[NV];
+  float4 v[NV];
   uint2 y[NV], z[NV];
-  ln_load_gb<NV>(a.g, a.b, gg, bb);  // with the row's loads, not after its sums
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = (i * 64 + lane) * 4;
@@ -178,7 +160,7 @@ __global__ __launch_bounds__(256) void layernorm_kernel(allie::LNArgs a) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) *reinterpret_cast<float4*>(a.h_out + src * d + (i * 64 + lane) * 4) = v[i];
   }
-  ln_row_store_gb<NV>(v, d, gg, bb, a.eps, a.y, r, a.act_bf16);
+  ln_row_store<NV>(v, d, a.g, a.b, a.eps, a.y, r, a.act_bf16);
 }
 
 // dst row r = src row idx[r], 16 bytes per thread

@@ -231,6 +231,12 @@ class Probe:
         self.capi = capi
         capi.check(capi.lib().allie_probe_begin(kind, max_launches), "probe")
 
+    def span(self):
+        """Time during which at least one probed launch ran (ms)."""
+        sp = C.c_float()
+        self.capi.check(self.capi.lib().allie_probe_span(C.byref(sp)), "probe span")
+        return sp.value
+
     def end(self):
         tot, n = C.c_float(), C.c_int()
         self.capi.check(self.capi.lib().allie_probe_end(C.byref(tot), C.byref(n)), "probe end")
@@ -263,19 +269,29 @@ def run_prefill(args, cfg, mode, workload):
     for _ in range(args.warmup):
         eng.prefill(words, lens, out=out)
     torch.cuda.synchronize()
-    probe = Probe(capi.PROBE_FC, args.steps * cfg.n_layer)
+    # a large batch runs as two halves (two launches per layer); room for up to four
+    probe = Probe(capi.PROBE_FC, 4 * args.steps * cfg.n_layer)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         eng.prefill(words, lens, out=out)
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
+    fc_span = probe.span()
     fc_tot, fc_n = probe.end()
     ms = el * 1000.0 / args.steps
     flops = alg_flops(cfg, lens)
-    fc_flops = 2.0 * T * cfg.d_ff * cfg.d_model
+    # the c_fc FLOPs of one forward: every row in the first L - 1 blocks, the
+    # games' last rows in the last block when it runs on those only (2 B <= T)
+    B = len(lens)
+    fc_rows = (cfg.n_layer - 1) * T + (B if 2 * B <= T else T)
+    fc_flops = 2.0 * fc_rows * cfg.d_ff * cfg.d_model
     fc_ms = fc_tot / max(fc_n, 1)
-    fc_tflops = fc_flops / (fc_ms * 1e-3) / 1e12
+    # a split batch's two halves run their c_fc launches on two streams, and
+    # those may overlap in time: the rate is the FLOPs over the time during
+    # which a c_fc launch was running (equal to the summed durations when no
+    # two overlap)
+    fc_tflops = args.steps * fc_flops / (fc_span * 1e-3) / 1e12
     res = base_result(args, len(lens) / (ms / 1000.0), "leaf evals/s", ms,
                       "bf16" if mode == "bfloat16" else "fp8 e4m3 weights, bf16 activations", workload,
                       n_seq=len(lens), n_tokens=T, tokens_per_s=T / (ms / 1000.0),
@@ -284,6 +300,18 @@ def run_prefill(args, cfg, mode, workload):
                       executed_tflop_per_step=executed_flops(cfg, lens) / 1e12,
                       whole_forward_mfma_frac_executed=executed_flops(cfg, lens) / (ms * 1e-3) / 1e12
                       / MFMA_BF16_PEAK_TFLOPS)
+    # the same kernel with the batch in one piece (no second stream beside it)
+    one_status = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    eng.prefill(words, lens, out=out, status=one_status)
+    torch.cuda.synchronize()
+    iso_steps = 3
+    probe = Probe(capi.PROBE_FC, iso_steps * cfg.n_layer)
+    for _ in range(iso_steps):
+        eng.prefill(words, lens, out=out, status=one_status)
+    torch.cuda.synchronize()
+    iso_span = probe.span()
+    iso_tot, iso_n = probe.end()
+    iso_tflops = iso_steps * fc_flops / (iso_span * 1e-3) / 1e12
     res["roofline"] = {
         "kernel": ("gemm_big_kernel<EPI_GELU> (MLP c_fc, persistent 256x256 tiles)" if mode == "bfloat16"
                    else "widen_fp8_kernel + gemm_big_kernel<EPI_GELU,SCALED> (MLP c_fc, fp8 weights "
@@ -293,7 +321,12 @@ def run_prefill(args, cfg, mode, workload):
         "traffic": read_traffic() if (mode == "bfloat16" and cfg.d_model == 1024) else None,
         "traffic_measured_on": traffic_commit() if (mode == "bfloat16" and cfg.d_model == 1024) else None,
         "avg_launch_ms": fc_ms, "launches": fc_n,
-        "alg_flop_per_launch": fc_flops,
+        "alg_flop_per_launch": args.steps * fc_flops / max(fc_n, 1),
+        "achieved_is": "c_fc FLOPs of the timed forwards / the time during which one of their c_fc launches ran",
+        "launch_span_ms": fc_span / args.steps, "launch_sum_ms": fc_tot / args.steps,
+        "one_piece": {"note": "the same forward with the batch in one piece on one stream",
+                      "avg_launch_ms": iso_tot / max(iso_n, 1), "launches": iso_n, "achieved": iso_tflops,
+                      "frac": iso_tflops / MFMA_BF16_PEAK_TFLOPS},
     }
     return res, eng, sd, seqs, lens, words, out
 

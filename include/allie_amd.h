@@ -153,7 +153,12 @@ typedef struct allie_outputs {
  * status (device int32[1], optional) receives the packer's bitmask (see
  * allie_pack_ragged): 4 a game longer than its kv_block_table row (its tail
  * is not cached), 8 the <PAD> id inside a game (the reference's padded batch
- * would mask that token, data.py:321; here it is an ordinary token). */
+ * would mask that token, data.py:321; here it is an ordinary token).
+ * A bf16 prefill of at least 24,576 tokens with neither kv_pool nor status
+ * runs as two halves of consecutive games on two streams of its own, forked
+ * from and joined back into `stream` (results as for one piece: rows never
+ * interact across games); it needs the workspace that
+ * allie_prefill_workspace_bytes reports, and runs in one piece on less. */
 size_t allie_prefill_workspace_bytes(const allie_model* m, int n_seq, int n_tokens);
 size_t allie_kv_block_bytes(const allie_model* m);
 int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_host, int n_seq,
@@ -248,6 +253,11 @@ enum {
   ALLIE_PROBE_DECODE    /* extend: the one-token-group (decode) attention kernel */
 };
 int allie_probe_begin(int kind, int max_launches);
+/* Before allie_probe_end: the time during which at least one probed launch
+ * ran (the union of their [start, end] intervals), which differs from the
+ * summed durations when launches on different streams overlap (a prefill
+ * split into two halves). */
+int allie_probe_span(float* span_ms_host);
 int allie_probe_end(float* total_ms_host, int* n_launches_host);
 
 /* Building blocks exported for tests and benchmarks.
