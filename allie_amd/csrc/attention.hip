@@ -115,19 +115,22 @@ __global__ __launch_bounds__(SEQ_WAVES * 64, 1) void attn_varlen_seq_kernel(Attn
     }
     float m = -INFINITY, lsum = 0.f;
     f32x16_t o[2] = {f32x16_t{}, f32x16_t{}};
-    for (int kb = 0; kb <= qt; ++kb) {
-      // ---- S^T = K Q^T for keys kb 32 .. + 31 ---------------------------------
-      f32x16_t st{};
-      {
-        const int krow = kb * 32 + ql;
-        const uint16_t* kr = sK + krow * HD;
-        const int sw = (krow >> 1) & 7;
+    auto load_k = [&](int kb, bf16x8_t (&kf)[4]) {
+      const int krow = kb * 32 + ql;
+      const uint16_t* kr = sK + krow * HD;
+      const int sw = (krow >> 1) & 7;
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          const bf16x8_t kf = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(kr + (((2 * kk + g) ^ sw) << 3)));
-          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], st, 0, 0, 0);
-        }
-      }
+      for (int kk = 0; kk < 4; ++kk)
+        kf[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(kr + (((2 * kk + g) ^ sw) << 3)));
+    };
+    // a block's key fragments are read while the previous block is scored
+    bf16x8_t kf[4];
+    load_k(0, kf);
+    for (int kb = 0; kb <= qt; ++kb) {
+      f32x16_t st{};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kk], qf[kk], st, 0, 0, 0);
+      load_k(kb < qt ? kb + 1 : kb, kf);  // (the last block re-reads its own, in bounds)
       // lane holds keys 8 (r / 4) + 4 g + r % 4 of the block for query ql
       if (kb == qt) {
 #pragma unroll
@@ -137,7 +140,7 @@ __global__ __launch_bounds__(SEQ_WAVES * 64, 1) void attn_varlen_seq_kernel(Attn
       float mx = st[0];
 #pragma unroll
       for (int r = 1; r < 16; ++r) mx = fmaxf(mx, st[r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = xor32_max(mx);
       const float m_new = fmaxf(m, mx);
       if (__builtin_amdgcn_ballot_w64(m_new > m) != 0) {
         const float alpha = __builtin_amdgcn_exp2f((m - m_new) * c2);  // m = -inf first: 0
@@ -184,7 +187,7 @@ __global__ __launch_bounds__(SEQ_WAVES * 64, 1) void attn_varlen_seq_kernel(Attn
     }
     // ---- normalise and store: lane holds dims 32 hb + 8 (r / 4) + 4 g + r % 4
     if (q0 + ql >= n) return;
-    const float inv = 1.0f / (lsum + __shfl_xor(lsum, 32, 64));
+    const float inv = 1.0f / xor32_sum(lsum);
     bf16_t* orow = out + (int64_t)(t0 + q0 + ql) * d + head * HD;
 #pragma unroll
     for (int hb = 0; hb < 2; ++hb)

@@ -539,8 +539,7 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
 #pragma unroll
       for (int db = 0; db < 4; ++db) vs[db] = *reinterpret_cast<const uint2*>(row + voff + 16 * db + 4 * lg);
     }
-    sdot += __shfl_xor(sdot, 16, 64);  // the query's four lane groups hold 16 dims each
-    sdot += __shfl_xor(sdot, 32, 64);
+    sdot = xor32_sum(xor16_sum(sdot));  // the query's four lane groups hold 16 dims each
     if (has_self) {
       m_run = sdot;
       l_run = lg == 0 ? 1.f : 0.f;  // the row sum is split over the lane groups
@@ -627,8 +626,7 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[kb][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = xor32_max(xor16_max(mx));
     const float m_new = fmaxf(m_run, mx);
     u32x4_t pf[2];  // P^T of k-step s: keys 32 s + 4 lg + {0..3}, then 32 s + 16 + 4 lg + {0..3}
     if (m_new != -INFINITY) {  // uniform per query
@@ -713,8 +711,7 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
     }
   }
   if (!q_ok) return;  // no barriers below
-  float l_tot = l_run + __shfl_xor(l_run, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
+  const float l_tot = xor32_sum(xor16_sum(l_run));
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   bf16_t* out = reinterpret_cast<bf16_t*>(a.out) + (int64_t)qi * d + head * HD + 4 * lg;
 #pragma unroll
@@ -913,8 +910,7 @@ __global__ __launch_bounds__(512, 4) void attn_extend_fan_kernel(ExtendAttnArgs 
         if (k0 + 16 * kb + 4 * lg + r >= lim || blk[kb] < 0) st[kb][r] = -INFINITY;
         mx = fmaxf(mx, st[kb][r]);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = xor32_max(xor16_max(mx));
     const float m_new = fmaxf(m_run, mx);
     u32x4_t pf[2];  // P^T of k-step s: keys 32 s + 4 lg + {0..3}, then 32 s + 16 + 4 lg + {0..3}
     if (m_new != -INFINITY) {  // uniform per query
@@ -968,8 +964,7 @@ __global__ __launch_bounds__(512, 4) void attn_extend_fan_kernel(ExtendAttnArgs 
 #pragma unroll
   for (int db = 0; db < 4; ++db)
     *reinterpret_cast<f32x4_t*>(so + lq * HD + (((4 * db + lg) ^ lq) << 2)) = o[db];
-  float l_tot = l_run + __shfl_xor(l_run, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
+  const float l_tot = xor32_sum(xor16_sum(l_run));
   if (lg == 0) {
     sML[wave * 32 + lq] = m_run;
     sML[wave * 32 + 16 + lq] = l_tot;

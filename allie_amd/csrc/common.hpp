@@ -63,6 +63,27 @@ ALLIE_DEV float fp8e4m3_to_f32(uint32_t v) {
 // fp8 e4m3fn -> bf16 bits (exact: 3 mantissa bits fit in bf16's 7)
 ALLIE_DEV uint32_t fp8e4m3_to_bf16(uint32_t v) { return __float_as_uint(fp8e4m3_to_f32(v)) >> 16; }
 
+// x combined with the x of lane l ^ 16 / l ^ 32 through gfx950's
+// v_permlane16_swap / v_permlane32_swap (lanes exchanged between 16-lane rows
+// / wave halves in registers, no LDS round trip as with a bpermute); both
+// lanes of a pair get the same bits (the lower lane's operand first).
+ALLIE_DEV float xor16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+ALLIE_DEV float xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+ALLIE_DEV float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+ALLIE_DEV float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 ALLIE_DEV float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
