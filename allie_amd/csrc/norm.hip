@@ -115,7 +115,7 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(allie::EmbedArgs a) {
 // a wait of their own)
 template <int NV, int ADD>
 __global__ __launch_bounds__(256) void layernorm_kernel(allie::LNArgs a) {
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t r = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   if (r >= a.rows_out) return;
   const int lane = threadIdx.x & 63;
   const int d = a.d;
