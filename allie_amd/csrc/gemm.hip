@@ -7,7 +7,8 @@
 // weights repacked once to [out][in] at load time.
 //
 // MFMA kernel: 256 threads (4 waves, 2 (m) x 2 (n)), block tile 256 (m) x 128
-// (n), two blocks per CU.  Each wave owns a 128 (m) x 64 (n) sub-tile = 2 x 4
+// (n) -- or 192 / 128 rows when M is small (gemm_tile_m) -- two blocks per
+// CU.  Each wave owns a 128 (m) x 64 (n) sub-tile = 2 x 4
 // MFMA 32x32x16 bf16 blocks (128 fp32 accumulators), which leaves room for a
 // second block on every SIMD: while one block sits in its epilogue, prologue
 // or a barrier, the other keeps the matrix cores busy.  (Measured on the
@@ -149,7 +150,7 @@ constexpr int W_FP8W = 3;
 
 template <int EPI, int WT, int OUT, int BMT>
 __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
-  // block tile BMT (256 or 128) x BN; wave (wm, wn) owns WMX x 64
+  // block tile BMT (128, 192 or 256) x BN; wave (wm, wn) owns WMX x 64
   constexpr int FMT = BMT / 64, WMX = BMT / 2, ASTG = BMT * BK, AI = BMT / 64;
   constexpr int STG = BMT == 128 ? 4 : STAGES;  // ring stages (128-row tiles: one more in flight)
   static_assert(4 * WMX * EP <= STG * (ASTG + W_STAGE), "epilogue region fits the ring");
@@ -412,12 +413,14 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
       // rows are issued before any store: a store may alias the next load, so
       // interleaving them would expose the memory latency 16 times.
       float* __restrict__ Rp = a.R;
+      constexpr int RG = WMX / 8;  // groups of 8 rows, 8 at a time
 #pragma unroll
-      for (int half8 = 0; half8 < WMX / 64; ++half8) {
+      for (int half8 = 0; half8 < (RG + 7) / 8; ++half8) {
         uint4 v[8];
         float4 h0[8], h1[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
+          if (half8 * 8 + u >= RG) break;
           const int ml = (half8 * 8 + u) * 8 + (lane >> 3);
           const int m = m0 + wm * WMX + ml;
           v[u] = *reinterpret_cast<const uint4*>(reg + ml * EP + cl);
@@ -429,6 +432,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_mfma_kernel(GemmArgs a) {
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
+          if (half8 * 8 + u >= RG) break;
           const int ml = (half8 * 8 + u) * 8 + (lane >> 3);
           const int m = m0 + wm * WMX + ml;
           if (m >= a.M) continue;
@@ -1175,24 +1179,27 @@ void launch_ev(K kernel, dim3 grid, dim3 block, hipStream_t st, hipEvent_t e0, h
     hipLaunchKernelGGL(kernel, grid, block, 0, st, args...);
 }
 
-// The 128- / 256-row MFMA kernel (and the split-K reduction), the product
-// timed by e0 / e1 when given.
+// The 128- / 192- / 256-row MFMA kernel (and the split-K reduction), the
+// product timed by e0 / e1 when given.
 template <int EPI, int WT, bool F32OUT>
 void launch_tiles(const GemmArgs& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   const int bm = gemm_tile_m(a.M, a.N);
   const int tiles = ((a.M + bm - 1) / bm) * (a.N / BN);
+  auto go = [&](auto kernel, int blocks) { launch_ev(kernel, dim3(blocks), dim3(NTHREADS), st, e0, e1, a); };
+  constexpr int OUT = F32OUT ? OUT_F32 : OUT_BF16;
   if (a.split > 1) {
-    if (bm == 128)
-      launch_ev(gemm_mfma_kernel<EPI, WT, OUT_PART, 128>, dim3(tiles * a.split), dim3(NTHREADS), st, e0, e1, a);
-    else
-      launch_ev(gemm_mfma_kernel<EPI, WT, OUT_PART, 256>, dim3(tiles * a.split), dim3(NTHREADS), st, e0, e1, a);
+    if (bm == 128) go(gemm_mfma_kernel<EPI, WT, OUT_PART, 128>, tiles * a.split);
+    else if (bm == 192) go(gemm_mfma_kernel<EPI, WT, OUT_PART, 192>, tiles * a.split);
+    else go(gemm_mfma_kernel<EPI, WT, OUT_PART, 256>, tiles * a.split);
     const int64_t n4 = (int64_t)a.M * (a.N / 4);
     hipLaunchKernelGGL((splitk_reduce_kernel<EPI, WT == W_FP8 || WT == W_FP8W, F32OUT>), dim3((unsigned)((n4 + 255) / 256)),
                        dim3(256), 0, st, a);
   } else if (bm == 128) {
-    launch_ev(gemm_mfma_kernel<EPI, WT, F32OUT ? OUT_F32 : OUT_BF16, 128>, dim3(tiles), dim3(NTHREADS), st, e0, e1, a);
+    go(gemm_mfma_kernel<EPI, WT, OUT, 128>, tiles);
+  } else if (bm == 192) {
+    go(gemm_mfma_kernel<EPI, WT, OUT, 192>, tiles);
   } else {
-    launch_ev(gemm_mfma_kernel<EPI, WT, F32OUT ? OUT_F32 : OUT_BF16, 256>, dim3(tiles), dim3(NTHREADS), st, e0, e1, a);
+    go(gemm_mfma_kernel<EPI, WT, OUT, 256>, tiles);
   }
 }
 
@@ -1308,8 +1315,15 @@ bool gemm_mfma_supported(const GemmArgs& a) {
 }
 
 int gemm_tile_m(int M, int N) {
-  // 256-row tiles unless that leaves fewer tiles than a 256-CU device has CUs
+  // 256-row tiles unless that leaves fewer tiles than a 256-CU device has
+  // CUs; 192-row ones where they fit one round of 256 and 128-row ones would
+  // not (a second, mostly empty round costs as much as a full one).  Kernel
+  // trace, weights cold, M = 1,450 (a C4 step): QKV 16.0 against 19.6 us,
+  // c_fc 19.9 against 23.7 us; at M = 512 and 4,096 192-row tiles were slower.
   const int64_t tiles256 = (int64_t)((M + 255) / 256) * (N / BN);
+  const int64_t tiles192 = (int64_t)((M + 191) / 192) * (N / BN);
+  const int64_t tiles128 = (int64_t)((M + 127) / 128) * (N / BN);
+  if (tiles128 > 256 && tiles192 <= 256) return 192;
   return tiles256 < 256 ? 128 : 256;
 }
 

@@ -135,8 +135,8 @@ bool gemm_uses_persistent(const GemmArgs& a);
 // true when launch_gemm writes this QKV GEMM's keys and values to a.kv_pool
 // itself (MFMA kernels with bf16 output); otherwise the caller copies them
 bool gemm_stores_kv(const GemmArgs& a);
-// block rows of the 256x128-class kernel for an M x N output: 256, or 128
-// when 256-row tiles would not cover a 256-CU device
+// block rows of the 256x128-class kernel for an M x N output: 256, 192 or
+// 128 (see gemm_tile_m)
 int gemm_tile_m(int M, int N);
 // K splits the forward uses for an M x N x K MFMA GEMM: enough blocks for
 // every CU when the output tiles alone leave most idle (small M)
