@@ -15,6 +15,7 @@ import torch
 from allie_amd import config, weights
 from allie_amd.engine import Engine, legal_mask
 from oracle.model_ref import RefModel, policy_summary
+from parity_floor import bf16_ulp
 
 pytestmark = pytest.mark.gpu
 
@@ -186,15 +187,25 @@ def medium():
 
 def test_prefill_medium_c2_subset(medium, cuda):
     """C2 (medium, bf16, 256 prefixes of 8..400): the full batch runs on the
-    GPU; 10 of its games are checked against the oracle's bf16 emulation."""
+    GPU (as two halves on two streams); 10 of its games are checked against
+    the oracle's bf16 emulation: logits before their final bf16 rounding,
+    value and time within 2e-2, the rounded logits within 2e-2 plus one bf16
+    ulp of their magnitude (two values under 2e-2 apart can round one ulp
+    further apart), top-1 as in check()."""
     cfg, sd = medium
     rng = np.random.default_rng(2)
     lens = rng.integers(8, 401, 256).astype(np.int32)
     seqs = [rng.integers(0, 1968, n).astype(np.uint32) for n in lens]
     eng = Engine(cfg, sd, mode="bfloat16")
-    got = run_engine(eng, seqs, lens)
+    got = run_engine(eng, seqs, lens, want_raw_logits=True)
     pick = [0, 1, 2, 3, int(np.argmax(lens)), int(np.argmin(lens)), 100, 200, 254, 255]
     ref = RefModel(cfg, sd, mode="bfloat16").forward_last([seqs[i].astype(np.int64) for i in pick])
     sub = {k: (v[pick] if v is not None else None) for k, v in got.items()}
-    check(sub, ref, 2e-2, "c2-bf16")
+    draw = np.abs(sub["logits_raw"] - ref["logits_raw"]).max()
+    over = np.abs(sub["logits"] - ref["logits"]) - (2e-2 + bf16_ulp(ref["logits"]))
+    print(f"c2-bf16: max|dlogit before rounding|={draw:.3g}, rounded logits past 2e-2 + 1 ulp: "
+          f"{int((over > 0).sum())}, past 2e-2: {int((np.abs(sub['logits'] - ref['logits']) > 2e-2).sum())}",
+          flush=True)
+    assert draw <= 2e-2 and (over <= 0).all()
+    check({**sub, "logits": sub["logits_raw"]}, {**ref, "logits": ref["logits_raw"]}, 2e-2, "c2-bf16")
     eng.close()
