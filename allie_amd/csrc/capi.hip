@@ -590,8 +590,14 @@ ExtendWS layout_extend(const allie_model* m, int n, int G, char* base, bool with
 }
 
 // A bf16 prefill of at least this many tokens (and no KV pool or status
-// output) runs as two halves on two streams
+// output) runs as two halves on two streams; so does an extend of as many
+// tokens in groups of several tokens each
 constexpr int64_t PREFILL_SPLIT_TOKENS = 24576;
+
+// *out = *a | *b (the validation flags of an extend's two halves)
+__global__ void or_status_kernel(int32_t* out, const int32_t* a, const int32_t* b) {
+  if (threadIdx.x == 0) *out = *a | *b;
+}
 
 // One prefill forward of n_seq games (T tokens) over the laid-out workspace
 // w, on stream st (arguments checked by allie_prefill).
@@ -1063,7 +1069,11 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
 
 size_t allie_extend_workspace_bytes(const allie_model* m, int n_tok, int n_groups) {
   if (!m || n_tok < 0 || n_groups < 0) return 0;
-  return layout_extend(m, n_tok, n_groups, nullptr, true).total;
+  size_t b = layout_extend(m, n_tok, n_groups, nullptr, true).total;
+  // room for the two halves of a split extend (see allie_prefill_workspace_bytes)
+  if (m->act_bf16 && n_tok >= PREFILL_SPLIT_TOKENS && n_groups >= 2)
+    b += layout_extend(m, 0, n_groups, nullptr, true).total + 32 * 256;
+  return b;
 }
 
 }  // extern "C"
@@ -1263,9 +1273,61 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   if (rc) return rc;
   if (!workspace) return fail(ALLIE_ERR_ARG, "bad extend arguments");
   ExtendWS w = layout_extend(m, n_tok, n_groups, (char*)workspace, true);
+  hipStream_t st = (hipStream_t)stream;
+  // A large extend of multi-token groups (MCTS tree levels) runs as two halves
+  // of consecutive groups on the model's two streams, as a large prefill does:
+  // groups never share keys they write, and each reads only its own prefix.
+  if (m->act_bf16 && plan.n1 == 0 && n_tok >= PREFILL_SPLIT_TOKENS && n_groups >= 2 && m->fork) {
+    int gc = 1;
+    while (gc < n_groups - 1 && 2 * (int64_t)group_start_host[gc] < n_tok) ++gc;
+    const int t0 = group_start_host[gc];
+    std::vector<int32_t> gs1((size_t)(n_groups - gc) + 1);
+    for (int g = gc; g <= n_groups; ++g) gs1[(size_t)(g - gc)] = group_start_host[g] - t0;
+    ExtendPlan p0, p1;
+    allie_outputs o1 = *out;
+    auto shift = [&](auto* q, int64_t k) { return q ? q + k : q; };
+    o1.logits = shift(out->logits, (int64_t)t0 * m->V);
+    o1.logits_raw = shift(out->logits_raw, (int64_t)t0 * m->V);
+    o1.value = out->value + t0;
+    o1.time = out->time + t0;
+    o1.top1 = out->top1 + t0;
+    o1.max_logit = out->max_logit + t0;
+    o1.lse = out->lse + t0;
+    const uint32_t* legal1 = legal ? legal + (int64_t)t0 * legal_words : nullptr;
+    const int32_t *ids1 = ids + t0, *pos1 = pos + t0, *pl1 = prefix_len + gc,
+                  *pb1 = prefix_blocks ? prefix_blocks + (int64_t)gc * max_blocks : nullptr,
+                  *es1 = extra_slot + (int64_t)t0 * max_extra, *ne1 = n_extra + t0;
+    if (!extend_check(m, ids, pos, t0, group_start_host, gc, prefix_len, prefix_blocks, max_blocks, extra_slot,
+                      n_extra, max_extra, legal, legal_words, out, kv_pool, kv_pool_blocks, &p0) &&
+        !extend_check(m, ids1, pos1, n_tok - t0, gs1.data(), n_groups - gc, pl1, pb1, max_blocks, es1, ne1,
+                      max_extra, legal1, legal_words, &o1, kv_pool, kv_pool_blocks, &p1)) {
+      const ExtendWS w0 = layout_extend(m, t0, gc, (char*)workspace, true);
+      const ExtendWS w1 = layout_extend(m, n_tok - t0, n_groups - gc, (char*)workspace + w0.total, true);
+      int dev = -1;
+      if (w0.total + w1.total <= workspace_bytes && hipGetDevice(&dev) == hipSuccess && dev == m->device) {
+        HIP_TRY(hipEventRecord(m->fork, st));
+        for (int i = 0; i < 2; ++i) HIP_TRY(hipStreamWaitEvent(m->side[i], m->fork, 0));
+        if ((rc = upload_i32(m, w0.group_start, group_start_host, (size_t)gc + 1, m->side[0]))) return rc;
+        if ((rc = extend_run(m, p0, w0, nullptr, ids, pos, t0, gc, prefix_len, prefix_blocks, max_blocks, extra_slot,
+                             n_extra, max_extra, temperature, legal, legal_words, out, kv_pool, kv_pool_blocks,
+                             nullptr, m->side[0])))
+          return rc;
+        if ((rc = upload_i32(m, w1.group_start, gs1.data(), gs1.size(), m->side[1]))) return rc;
+        if ((rc = extend_run(m, p1, w1, nullptr, ids1, pos1, n_tok - t0, n_groups - gc, pl1, pb1, max_blocks, es1, ne1,
+                             max_extra, temperature, legal1, legal_words, &o1, kv_pool, kv_pool_blocks, nullptr,
+                             m->side[1])))
+          return rc;
+        for (int i = 0; i < 2; ++i) {
+          HIP_TRY(hipEventRecord(m->join[i], m->side[i]));
+          HIP_TRY(hipStreamWaitEvent(st, m->join[i], 0));
+        }
+        if (status) hipLaunchKernelGGL(or_status_kernel, dim3(1), dim3(64), 0, st, status, w0.status, w1.status);
+        return ALLIE_OK;
+      }
+    }
+  }
   if (workspace_bytes < w.total)
     return fail(ALLIE_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, w.total);
-  hipStream_t st = (hipStream_t)stream;
   if ((rc = upload_i32(m, w.group_start, group_start_host, (size_t)n_groups + 1, st))) return rc;
   return extend_run(m, plan, w, nullptr, ids, pos, n_tok, n_groups, prefix_len, prefix_blocks, max_blocks,
                     extra_slot, n_extra, max_extra, temperature, legal, legal_words, out, kv_pool, kv_pool_blocks,

@@ -446,14 +446,16 @@ def bench_c3(args):
         times, attn = [], {}
         for k in range(1, lay.depth + 1):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            p = Probe(capi.PROBE_ATTN, cfg.n_layer) if k in probe_levels else None
+            # a large level runs as two halves: two launches per layer
+            p = Probe(capi.PROBE_ATTN, 2 * cfg.n_layer) if k in probe_levels else None
             e0.record()
             outs[k - 1] = tx.expand_level(k, out=outs[k - 1])
             e1.record()
             torch.cuda.synchronize()
             times.append(e0.elapsed_time(e1))
             if p:
-                attn[k] = p.end()
+                span = p.span()
+                attn[k] = p.end() + (span,)
         return times, attn
 
     for _ in range(max(args.warmup, 1)):
@@ -471,15 +473,19 @@ def bench_c3(args):
     for k in (1, 2, 4):
         n = lay.level_size(k)
         bytes_ = lay.n_roots * P * kv_tok + n * k * kv_tok + n * 2 * d * 2
-        tot, cnt = attn[k]
-        ms = tot / max(cnt, 1)
-        roof[k] = {"avg_launch_ms": ms, "alg_bytes_per_launch": bytes_, "achieved_GBs": bytes_ / (ms * 1e-3) / 1e9}
+        tot, cnt, span = attn[k]
+        # per layer: the time during which the layer's attention launches ran (the
+        # union of their intervals; two overlapping launches when the level runs as
+        # two halves on two streams, one otherwise)
+        ms = span / L
+        roof[k] = {"ms_per_layer": ms, "avg_launch_ms": tot / max(cnt, 1), "launches_per_layer": cnt / L,
+                   "alg_bytes_per_layer": bytes_, "achieved_GBs": bytes_ / (ms * 1e-3) / 1e9}
     # level 4: every pool row once (ancestors shared by siblings), and its MFMA work
     n4 = lay.level_size(4)
     uniq = lay.n_roots * P * kv_tok + sum(lay.level_size(j) for j in range(1, 5)) * kv_tok + n4 * 2 * d * 2
     fl4 = 4 * d * n4 * (P + 4)  # QK^T and PV over each node's P + 4 keys
-    roof[4].update(unique_bytes_per_launch=uniq, achieved_unique_GBs=uniq / (roof[4]["avg_launch_ms"] * 1e-3) / 1e9,
-                   alg_flop_per_launch=fl4, achieved_TFLOPs=fl4 / (roof[4]["avg_launch_ms"] * 1e-3) / 1e12)
+    roof[4].update(unique_bytes_per_layer=uniq, achieved_unique_GBs=uniq / (roof[4]["ms_per_layer"] * 1e-3) / 1e9,
+                   alg_flop_per_layer=fl4, achieved_TFLOPs=fl4 / (roof[4]["ms_per_layer"] * 1e-3) / 1e12)
     total_ms = float(level_ms.sum())
     leaves = lay.level_size(lay.depth)
     flops = sum(2 * cfg.linear_params * lay.level_size(k) + 4 * d * L * lay.level_size(k) * (P + k)
