@@ -374,6 +374,138 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 4 : 1) void attn_extend_wave_
   }
 }
 
+// Split decode kernel (bf16, one-token groups: token i is group i): one
+// workgroup of NWV waves per (token, head), for batches with too few
+// (token, head) rows to fill the device with one wave each.  An MCTS leaf
+// has 16 rows: one wave per row walks its 5-8 key chunks one after another,
+// each a dependent round trip to memory, while here wave w takes chunks
+// w, w + NWV, ... so every chunk is requested at once.  Keys, visibility and
+// rounding points are the wave kernel's (lane l holds key l / 4 of a chunk
+// and head dims 16 (l % 4) .. +15; P rounded to bf16 for the product with V,
+// the row sum unrounded); each wave keeps its own running max, and the waves'
+// (max, sum, 64 accumulators) are combined through LDS.
+template <int NWV>
+__global__ __launch_bounds__(NWV * 64) void attn_extend_split_kernel(ExtendAttnArgs a) {
+  const int H = a.n_head, d = H * HD;
+  const int i = blockIdx.x / H, head = blockIdx.x - (blockIdx.x / H) * H;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kj = lane >> 2, dq = (lane & 3) * 16;
+  const bf16_t* __restrict__ qkv = reinterpret_cast<const bf16_t*>(a.qkv);
+  const bf16_t* __restrict__ pool = reinterpret_cast<const bf16_t*>(a.pool);
+  const float sl2 = a.scale * 1.4426950408889634f;  // scale * log2(e)
+  Row16<bf16_t> qr;
+  fetch16<bf16_t>(qkv + (int64_t)i * 3 * d + head * HD + dq, qr);
+  const int P = min(a.prefix_len[i], a.pos[i]);
+  int nbp = (P + KV_BLOCK - 1) / KV_BLOCK;
+  nbp = nbp < a.max_blocks ? nbp : a.max_blocks;
+  int E = a.n_extra[i];
+  E = E < 0 ? 0 : (E > a.max_extra ? a.max_extra : E);
+  const int nch = nbp + (E + KV_BLOCK - 1) / KV_BLOCK;
+  const int32_t* btab = a.prefix_blocks + (int64_t)i * a.max_blocks;
+  // as in the wave kernel: a key that is not visible reads a written row
+  // (the block's first position, or the token's own slot) and gets p = 0
+  auto locate = [&](int c, int64_t& off, bool& ok) {
+    int blk, kpos;
+    if (c < nbp) {
+      blk = btab[c];
+      ok = c * KV_BLOCK + kj < P;
+      kpos = ok ? kj : 0;
+    } else {
+      const int e = (c - nbp) * KV_BLOCK + kj;
+      const int sl = a.extra_slot[(int64_t)i * a.max_extra + min(e, E - 1)];
+      blk = sl >> 4;
+      kpos = sl & 15;
+      ok = e < E && sl >= 0;
+    }
+    const bool in_pool = blk >= 0 && blk < a.pool_blocks;
+    ok = ok && in_pool;
+    off = pool_off(in_pool ? blk : 0, a.pool_blocks, a.layer, 0, H, head, in_pool ? kpos : 0) + dq;
+  };
+  float m_run = -INFINITY, l_run = 0.f, acc[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.f;
+  const int64_t voff = (int64_t)H * KV_BLOCK * HD;
+  auto reduce_chunk = [&](const Row16<bf16_t>& kr, const Row16<bf16_t>& vr, bool ok) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t qw[4] = {qr.v[j].x, qr.v[j].y, qr.v[j].z, qr.v[j].w};
+      const uint32_t kw[4] = {kr.v[j].x, kr.v[j].y, kr.v[j].z, kr.v[j].w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qw[t]), __builtin_bit_cast(bf16x2_t, kw[t]), s,
+                                            false);
+    }
+    s *= sl2;
+    s += dpp_f<0xb1>(s);  // the 4 lanes of a key sum their dims
+    s += dpp_f<0x4e>(s);
+    s = ok ? s : -INFINITY;
+    float mb = fmaxf(s, dpp_f<0x124>(s));  // max over the row's 4 keys, then the 4 rows
+    mb = fmaxf(mb, dpp_f<0x128>(mb));
+    mb = fmaxf(fmaxf(readlane_f(mb, 0), readlane_f(mb, 16)), fmaxf(readlane_f(mb, 32), readlane_f(mb, 48)));
+    const float m_new = fmaxf(m_run, mb);
+    if (m_new == -INFINITY) return;  // nothing visible yet (wave-uniform)
+    const float alpha = exp2f(m_run - m_new);
+    const float p = ok ? exp2f(s - m_new) : 0.f;
+    l_run = l_run * alpha + ((lane & 3) == 0 ? p : 0.f);
+    const float pv = round_bf16(p);
+    float vv[16];
+    widen16<bf16_t>(vr, vv);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = acc[j] * alpha + pv * vv[j];
+    m_run = m_new;
+  };
+  auto fetch_chunk = [&](int c, Row16<bf16_t>& kr, Row16<bf16_t>& vr, bool& ok) {
+    int64_t off;
+    locate(c, off, ok);
+    fetch16<bf16_t>(pool + off, kr);
+    fetch16<bf16_t>(pool + off + voff, vr);
+  };
+  // two register buffers: this wave's next chunk loads while one is reduced
+  Row16<bf16_t> kA, vA, kB, vB;
+  bool okA = false, okB = false;
+  if (wave < nch) fetch_chunk(wave, kA, vA, okA);
+  for (int c = wave; c < nch; c += 2 * NWV) {
+    if (c + NWV < nch) fetch_chunk(c + NWV, kB, vB, okB);
+    reduce_chunk(kA, vA, okA);
+    if (c + NWV >= nch) break;
+    if (c + 2 * NWV < nch) fetch_chunk(c + 2 * NWV, kA, vA, okA);
+    reduce_chunk(kB, vB, okB);
+  }
+  // the wave's 16 key lanes of each head-dim group, then its 4 groups' sums
+#pragma unroll
+  for (int o = 4; o < 64; o <<= 1) {
+    l_run += __shfl_xor(l_run, o, 64);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] += __shfl_xor(acc[j], o, 64);
+  }
+  l_run += __shfl_xor(l_run, 1, 64);
+  l_run += __shfl_xor(l_run, 2, 64);
+  __shared__ float s_m[NWV], s_l[NWV], s_acc[NWV][HD];
+  if (lane == 0) {
+    s_m[wave] = m_run;
+    s_l[wave] = l_run;
+  }
+  if (kj == 0) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s_acc[wave][dq + j] = acc[j];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < NWV; ++w) mx = fmaxf(mx, s_m[w]);
+  float l_tot = 0.f, o = 0.f;
+#pragma unroll
+  for (int w = 0; w < NWV; ++w) {
+    const float f = s_m[w] == -INFINITY ? 0.f : exp2f(s_m[w] - mx);  // a wave that saw no visible key adds 0
+    l_tot += s_l[w] * f;
+    o += s_acc[w][lane] * f;
+  }
+  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  reinterpret_cast<bf16_t*>(a.out)[(int64_t)i * d + head * HD + lane] = (bf16_t)f2bf(o * inv);
+}
+
 // ---------------------------------------------------------------------------
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
@@ -1050,6 +1182,15 @@ hipError_t launch_attn_extend_wave(const ExtendAttnArgs& a, hipStream_t st) {
     launch_timed(attn_extend_wave_kernel<bf16_t>, grid, dim3(256), 0, st, a);
   else
     launch_timed(attn_extend_wave_kernel<float>, grid, dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_extend_split(const ExtendAttnArgs& a, hipStream_t st) {
+  if (!a.act_bf16) return hipErrorInvalidValue;
+  const int64_t rows = (int64_t)a.n * a.n_head;
+  if (rows == 0) return hipSuccess;
+  if (rows > DECODE_SPLIT_MAX_ROWS) return hipErrorInvalidValue;
+  launch_timed(attn_extend_split_kernel<8>, dim3((unsigned)rows), dim3(8 * 64), 0, st, a);
   return hipGetLastError();
 }
 

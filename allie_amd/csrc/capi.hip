@@ -302,9 +302,28 @@ struct KVDest {
   int layer, pool_blocks;
 };
 
+// A skinny GEMM's A operand as the LayerNorm of rows of h (GemmArgs::ln_h)
+struct LNSrc {
+  const float* h;
+  const int32_t* row;  // gather (row m is h row row[m]) or null
+  const float* g;
+  const float* b;
+};
+
+int wtype_of(const allie_model* m) {
+  return m->cfg.mode == ALLIE_MODE_FP32 ? W_F32 : (m->cfg.mode == ALLIE_MODE_FP8W ? W_FP8 : W_BF16);
+}
+
+// Whether the M x N x K projection of this model after a LayerNorm takes that
+// LayerNorm in its prologue (the skinny kernel, bf16 activations): then the
+// LayerNorm kernel is not launched and the projection reads h instead of x.
+bool ln_fused(const allie_model* m, int M, int N, int K, int wtype) {
+  return m->act_bf16 && gemm_skinny_ln_ok(M, N, K, wtype);
+}
+
 int gemm(const allie_model* m, const void* A, const void* W, const float* bias, const float* scale,
          void* C, float* R, int M, int N, int K, int epi, int probe_kind, float* part, void* wdq, hipStream_t st,
-         const KVDest* kv = nullptr, bool* kv_done = nullptr) {
+         const KVDest* kv = nullptr, bool* kv_done = nullptr, const LNSrc* ln = nullptr) {
   GemmArgs g{};
   g.A = A;
   g.W = W;
@@ -319,11 +338,18 @@ int gemm(const allie_model* m, const void* A, const void* W, const float* bias, 
   g.ldc = N;
   g.ldr = N;
   g.epi = epi;
-  g.wtype = m->cfg.mode == ALLIE_MODE_FP32 ? W_F32 : (m->cfg.mode == ALLIE_MODE_FP8W ? W_FP8 : W_BF16);
+  g.wtype = wtype_of(m);
   g.out_f32 = m->cfg.mode == ALLIE_MODE_FP32;
   g.split = (part && g.wtype != W_F32) ? gemm_split_factor(M, N, K) : 1;
   g.part = part;
   g.wdq = g.wtype == W_FP8 ? wdq : nullptr;
+  if (ln) {
+    g.ln_h = ln->h;
+    g.ln_row = ln->row;
+    g.ln_g = ln->g;
+    g.ln_b = ln->b;
+    g.ln_eps = m->cfg.eps;
+  }
   if (kv) {
     g.kv_pool = kv->pool;
     g.kv_slot = kv->slot;
@@ -406,6 +432,9 @@ int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slo
   *final_add = nullptr;
   *h_final = w.h;
   int rc;
+  // the next layer's ln_1 is left to its QKV projection's prologue (the
+  // first layer's is fused into the embedding)
+  bool ln1_in_qkv = false;
   // c_proj, ln_2 and the MLP of layer li over M rows (attention output in
   // attn, residual stream h), then the next layer's ln_1 into x
   auto finish = [&](int li, int M, void* attn_in, void* x, float* h, void* ff) -> int {
@@ -436,8 +465,14 @@ int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slo
     ln.b = l.ln2_b;
     ln.add = fuse_proj ? y_attn : nullptr;
     ln.h_out = (fuse_proj && !defer) ? h : nullptr;
-    HIP_TRY(launch_layernorm(ln, st));
-    if ((r = gemm(m, x, l.w_fc, l.b_fc, l.s_fc, ff, nullptr, M, 4 * d, d, EPI_GELU, ALLIE_PROBE_FC, w.part, w.wdq, st))) return r;
+    // a plain ln_2 (the residual add already in h) before a skinny c_fc runs
+    // in that GEMM's prologue
+    const LNSrc ln2{h, nullptr, l.ln2_g, l.ln2_b};
+    const bool ln2_in_fc = !fuse_proj && ln_fused(m, M, 4 * d, d, wtype_of(m));
+    if (!ln2_in_fc) HIP_TRY(launch_layernorm(ln, st));
+    if ((r = gemm(m, x, l.w_fc, l.b_fc, l.s_fc, ff, nullptr, M, 4 * d, d, EPI_GELU, ALLIE_PROBE_FC, w.part, w.wdq, st,
+                  nullptr, nullptr, ln2_in_fc ? &ln2 : nullptr)))
+      return r;
     if (fuse_fc2) {
       if ((r = gemm(m, ff, l.w_pr, l.b_pr, l.s_pr, x, nullptr, M, d, 4 * d, EPI_STORE, ALLIE_PROBE_FC2, w.part, w.wdq, st))) return r;
     } else {
@@ -449,7 +484,9 @@ int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slo
       ln.add = fuse_fc2 ? (defer ? y_attn : x) : nullptr;
       ln.add2 = defer ? x : nullptr;
       ln.h_out = fuse_fc2 ? h : nullptr;
-      HIP_TRY(launch_layernorm(ln, st));
+      // likewise a plain ln_1 before a skinny QKV projection
+      ln1_in_qkv = !fuse_fc2 && ln_fused(m, M, 3 * d, d, wtype_of(m));
+      if (!ln1_in_qkv) HIP_TRY(launch_layernorm(ln, st));
     } else {
       *final_add = fuse_fc2 ? x : nullptr;
     }
@@ -459,9 +496,12 @@ int run_layers(const allie_model* m, const Acts& w, int T, const int32_t* kv_slo
     const LayerW& l = m->layers[li];
     const KVDest kvd{kv_pool, kv_slot, li, kv_pool_blocks};
     bool kv_done = false;
+    const LNSrc ln1{w.h, nullptr, l.ln1_g, l.ln1_b};
     if ((rc = gemm(m, w.x, l.w_qkv, l.b_qkv, l.s_qkv, w.qkv, nullptr, T, 3 * d, d, EPI_STORE, ALLIE_PROBE_QKV, w.part,
-                   w.wdq, st, (kv_only_pool && kv_pool && kv_slot) ? &kvd : nullptr, &kv_done)))
+                   w.wdq, st, (kv_only_pool && kv_pool && kv_slot) ? &kvd : nullptr, &kv_done,
+                   ln1_in_qkv ? &ln1 : nullptr)))
       return rc;
+    ln1_in_qkv = false;
     if (kv_pool && kv_slot && !kv_done) {
       KVWriteArgs kw{};
       kw.qkv = w.qkv;
@@ -509,9 +549,19 @@ int run_heads(const allie_model* m, const float* h, const void* h_add, const int
   lf.eps = m->cfg.eps;
   lf.y = hx;
   lf.act_bf16 = act;
-  HIP_TRY(launch_layernorm(lf, st));
+  // ln_f in the heads GEMM's prologue when that GEMM is skinny and no
+  // residual add is pending
+  const bool lnf_in_gemm = !h_add && ln_fused(m, rows, m->NH, d, W_BF16);
+  if (!lnf_in_gemm) HIP_TRY(launch_layernorm(lf, st));
   {
     GemmArgs g{};
+    if (lnf_in_gemm) {
+      g.ln_h = h;
+      g.ln_row = row_idx;
+      g.ln_g = m->lnf_g;
+      g.ln_b = m->lnf_b;
+      g.ln_eps = m->cfg.eps;
+    }
     g.A = hx;
     g.W = m->w_head;
     g.bias = m->b_head;
@@ -1217,11 +1267,15 @@ int extend_run(allie_model* m, const ExtendPlan& plan, const ExtendWS& w, const 
   // one-token groups (decode steps) [0, n_dec) stream their keys with one
   // wave per (token, head), the games with the most keys first (bf16)
   const int n_dec = tree ? n1 : (xa.one_token_groups ? n_tok : 0);
-  if (act && n_dec > 0) HIP_TRY(launch_decode_order(xa, n_dec, w.order, st));
+  // too few (token, head) rows to fill the device with one wave each (an
+  // MCTS leaf: 16): a workgroup of waves splits each row's keys
+  const bool split_dec = act && n_dec > 0 && (int64_t)n_dec * m->H <= DECODE_SPLIT_MAX_ROWS;
+  if (act && n_dec > 0 && !split_dec) HIP_TRY(launch_decode_order(xa, n_dec, w.order, st));
   auto launch_decode = [&](int nd) -> hipError_t {
     ExtendAttnArgs wa = xa;
     wa.n = nd == n_groups ? n_tok : nd;
     wa.one_token_groups = nd == n_groups ? xa.one_token_groups : 1;
+    if (split_dec) return launch_attn_extend_split(wa, st);
     wa.order = (act && wa.one_token_groups) ? w.order : nullptr;
     return launch_attn_extend_wave(wa, st);
   };

@@ -84,6 +84,22 @@ ALLIE_DEV float xor32_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// sum over the wave in registers: DPP within rows of 16 lanes (xor 1, 2,
+// then half-row and row mirrors), then across rows by v_permlane16/32_swap;
+// no LDS instruction (wave_sum's shuffles are ds_bpermute round trips).  Every
+// lane gets the same bits.
+template <int CTRL>
+ALLIE_DEV float dpp_mov_f(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+ALLIE_DEV float wave_sum_regs(float v) {
+  v += dpp_mov_f<0xb1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_mov_f<0x4e>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_mov_f<0x141>(v);  // row_half_mirror: lane i + lane 7 - i of each 8
+  v += dpp_mov_f<0x140>(v);  // row_mirror: lane i + lane 15 - i of each 16
+  return xor32_sum(xor16_sum(v));
+}
+
 ALLIE_DEV float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -1303,8 +1303,9 @@ bool gemm_uses_persistent(const GemmArgs& a) {
 
 bool gemm_stores_kv(const GemmArgs& a) {
   if (!a.kv_pool || !a.kv_slot || a.M <= 0 || a.epi != EPI_STORE || a.out_f32 || a.wtype == W_F32) return false;
-  if (a.N % 192 != 0 || a.ldc != a.N || a.split > 1 || gemm_skinny_supported(a) || !gemm_mfma_supported(a))
-    return false;
+  if (a.N % 192 != 0 || a.ldc != a.N) return false;
+  if (gemm_skinny_supported(a)) return true;  // the skinny kernel writes C and the pool
+  if (a.split > 1 || !gemm_mfma_supported(a)) return false;
   // the persistent kernel addresses one layer's slice with 32-bit offsets
   const bool big = use_big(a, a.wtype, a.out_f32 != 0);
   return !big || (int64_t)a.kv_pool_blocks * 2 * (a.N / 192) * 2048 < ((int64_t)1 << 32);
@@ -1350,6 +1351,7 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t st) {
   if (a.M == 0) return hipSuccess;
   if (a.kv_pool && !gemm_stores_kv(a)) return hipErrorInvalidValue;
   if (a.wtype != W_F32 && gemm_skinny_supported(a)) return launch_gemm_skinny(a, st);
+  if (a.ln_h) return hipErrorInvalidValue;  // the LayerNorm prologue exists on the skinny kernel only
   if (a.wtype == W_F32) {
     dim3 grid((a.N + 63) / 64, (a.M + 63) / 64);
     switch (a.epi) {

@@ -114,11 +114,23 @@ struct GemmArgs {
                        // persistent kernel (large M), or null
   // An extend's QKV projection (EPI_STORE, N = 3 d): with kv_pool set the key
   // and value columns [d, 3 d) of row m go to pool slot kv_slot[m] of layer
-  // kv_layer ([layer][kv_pool_blocks][k|v][head][16][64] bf16) instead of C;
-  // rows with a slot outside the pool are not written (see gemm_stores_kv)
+  // kv_layer ([layer][kv_pool_blocks][k|v][head][16][64] bf16) instead of C
+  // (the skinny kernel writes them to C as well); rows with a slot outside
+  // the pool are not written (see gemm_stores_kv)
   void* kv_pool;
   const int32_t* kv_slot;
   int kv_layer, kv_pool_blocks;
+  // Skinny kernel only: with ln_h set, A is not read; the A operand is the
+  // LayerNorm of rows of ln_h (fp32 [*][K]; row m is ln_h row ln_row[m], or m
+  // when ln_row is null) with gamma ln_g, beta ln_b and eps ln_eps, rounded to
+  // bf16.  Every workgroup computes it into LDS with launch_layernorm's lane
+  // layout and summation order, so the operand equals what that kernel
+  // writes, bit for bit (see gemm_skinny_ln_ok).
+  const float* ln_h;
+  const int32_t* ln_row;
+  const float* ln_g;
+  const float* ln_b;
+  float ln_eps;
 };
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t st);
 bool gemm_mfma_supported(const GemmArgs& a);
@@ -126,6 +138,11 @@ bool gemm_mfma_supported(const GemmArgs& a);
 // streams the weights once (launch_gemm picks it for such shapes)
 constexpr int SKINNY_MAX_M = 8;
 bool gemm_skinny_supported(const GemmArgs& a);
+// whether an M x N x K GEMM with bf16 or fp8 weights (wtype) runs on the
+// skinny kernel with its A operand's LayerNorm in the prologue (ln_h): K a
+// multiple of 256 of at most SKINNY_LN_MAX_K
+constexpr int SKINNY_LN_MAX_K = 2048;
+bool gemm_skinny_ln_ok(int M, int N, int K, int wtype);
 hipError_t launch_gemm_skinny(const GemmArgs& a, hipStream_t st);
 // true when this GEMM runs on the persistent 256 x 256 kernel (large M,
 // bf16 weights or fp8 with wdq, store or gelu epilogue); the forward then writes attention
@@ -133,7 +150,8 @@ hipError_t launch_gemm_skinny(const GemmArgs& a, hipStream_t st);
 // stream in the following LayerNorm
 bool gemm_uses_persistent(const GemmArgs& a);
 // true when launch_gemm writes this QKV GEMM's keys and values to a.kv_pool
-// itself (MFMA kernels with bf16 output); otherwise the caller copies them
+// itself (MFMA kernels with bf16 output, and the skinny kernel); otherwise the
+// caller copies them
 bool gemm_stores_kv(const GemmArgs& a);
 // block rows of the 256x128-class kernel for an M x N output: 256, 192 or
 // 128 (see gemm_tile_m)
@@ -210,6 +228,11 @@ struct ExtendAttnArgs {
 };
 // one wave per (token, head), any group sizes, bf16 or fp32
 hipError_t launch_attn_extend_wave(const ExtendAttnArgs& a, hipStream_t st);
+// one workgroup of waves per (token, head) of one-token groups (bf16), the
+// waves splitting the keys: for batches of at most DECODE_SPLIT_MAX_ROWS
+// (token, head) rows, too few to fill the device with one wave per row
+constexpr int DECODE_SPLIT_MAX_ROWS = 256;
+hipError_t launch_attn_extend_split(const ExtendAttnArgs& a, hipStream_t st);
 // order[0 .. n) of the one-token groups 0 .. n - 1, most keys first
 hipError_t launch_decode_order(const ExtendAttnArgs& a, int n, int32_t* order, hipStream_t st);
 // MFMA tiles of tile_q queries sharing a group's prefix, private keys as

@@ -190,14 +190,31 @@ class Policy(DecodeStrategy):
 
 
 class MCTSNode:
-    """decode.py:273-306."""
+    """decode.py:273-306.  A child made at expansion holds its parent's game
+    and its move, and builds its own game (``parent.make_move(move)``) the
+    first time it is read: a node has about 30 children, of which a search
+    reads few."""
 
-    def __init__(self, prior: float, game: Game):
+    # the KV-cached search's per-node fields (allie_amd.search_kv) included
+    __slots__ = ("prior", "children", "visit_count", "value_sum", "_game", "_from", "_kv_parent", "_kv_token",
+                 "_kv_path", "_kv_eval", "__dict__")
+
+    def __init__(self, prior: float, game: Optional[Game] = None, parent_game: Optional[Game] = None,
+                 move: Optional[str] = None):
         self.prior = prior
         self.children: dict[str, "MCTSNode"] = {}
         self.visit_count = 0
         self.value_sum = 0.0
-        self.game = game
+        self._game = game
+        self._from = None if game is not None else (parent_game, move)
+
+    @property
+    def game(self) -> Game:
+        if self._game is None:
+            parent_game, move = self._from
+            self._game = parent_game.make_move(move)
+            self._from = None
+        return self._game
 
     @property
     def board(self):
@@ -303,8 +320,9 @@ class MCTS(Policy):
 
     def _expand(self, node: MCTSNode, policy: list) -> None:
         kv = self._kv if self._kv is not None and self._kv.active else None
+        game = node.game
         for action, prior in zip(node.legal_moves, policy):
-            child = MCTSNode(prior, node.game.make_move(action))
+            child = MCTSNode(prior, parent_game=game, move=action)
             if kv is not None:
                 kv.attach(node, child, action)
             node.children[action] = child
@@ -318,7 +336,20 @@ class MCTS(Policy):
         return 0.0 if self.dummy_value_function else value
 
     def select_child(self, node: MCTSNode) -> MCTSNode:
-        return max(node.children.values(), key=lambda child: self.ucb_score(node, child))
+        """The first child of maximal ``ucb_score`` (as max() picks it),
+        with ucb_score's arithmetic in its order and the parent's terms
+        computed once."""
+        if type(self).ucb_score is not MCTS.ucb_score:
+            return max(node.children.values(), key=lambda child: self.ucb_score(node, child))
+        pb_base = math.log((node.visit_count + self.c_base + 1) / self.c_base) + self.c_puct
+        sq = math.sqrt(node.visit_count)
+        best, best_s = None, None
+        for child in node.children.values():
+            n = child.visit_count
+            s = pb_base * (sq / (1 + n)) * child.prior + (child.value_sum / n if n else 0.0)
+            if best is None or s > best_s:
+                best, best_s = child, s
+        return best
 
     def ucb_score(self, parent: MCTSNode, child: MCTSNode) -> float:
         pb_c = math.log((parent.visit_count + self.c_base + 1) / self.c_base) + self.c_puct
