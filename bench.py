@@ -631,6 +631,7 @@ def bench_search(args):
     modes = {"recompute": {}, "kv": {"kv_cache": True}, "kv_eager": {"kv_cache": True, "kv_graph": False},
              "kv_batch16": {"kv_cache": True, "leaf_batch": 16}}
     ms = {}
+    leaf_us = None
     for name, kw in modes.items():
         strat = DECODE_STRATEGIES["mcts"](model, tok, device="cuda", precision="bfloat16", n_sims=n_sims, **kw)
         for g in games[: args.warmup]:
@@ -641,6 +642,18 @@ def bench_search(args):
             strat.score_full(g, g.legal_moves)
         torch.cuda.synchronize()
         ms[name] = (time.perf_counter() - t0) * 1000.0 / args.steps
+        if name == "kv":
+            # GPU time of one leaf: the captured graph replayed with the last
+            # leaf's inputs (it rewrites that leaf's keys and values with the
+            # same numbers), timed by events on the replay stream
+            lg = strat._kv.leaf_graph
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(100):
+                lg.graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            leaf_us = e0.elapsed_time(e1) * 10.0
     model.close()
     res = base_result(args, n_sims / (ms["kv"] / 1000.0), "simulations/s", ms["kv"], "bf16",
                       "MCTS decision: medium 24x1024x16, 50 simulations, roots = random legal games of 60 plies "
@@ -648,6 +661,7 @@ def bench_search(args):
                       ms_per_decision={k: round(v, 2) for k, v in ms.items()},
                       sims_per_s={k: round(n_sims / (v / 1000.0), 1) for k, v in ms.items()},
                       speedup_kv_vs_recompute=ms["recompute"] / ms["kv"],
+                      kv_leaf_gpu_us=round(leaf_us, 1),
                       note="kv replays each leaf from a captured HIP graph, kv_eager launches it kernel by "
                            "kernel; kv_batch16 is a different (virtual-loss batched) search; recompute, kv and "
                            "kv_eager make the same decisions")

@@ -105,6 +105,37 @@ def test_decode_long_games(tiny, cuda):
     eng.close()
 
 
+@pytest.mark.parametrize("mode", ["bfloat16", "fp8w"])
+def test_single_token_chain_matches_full_recompute(tiny, mode, cuda):
+    """An MCTS search path evaluated one leaf at a time (one token, one
+    group: the QKV projection runs the token's attention in its tail): a
+    root prefilled into the pool, then four tokens, each over the root's
+    blocks plus its ancestors' scattered private slots and its own, against
+    the full recompute of root + path (2e-2, top-1 rule)."""
+    cfg, sd = tiny
+    rng = np.random.default_rng(21)
+    P = 45
+    root = list(rng.integers(0, 1968, P))
+    eng = Engine(cfg, sd, mode=mode)
+    pool = nan_pool(eng, 3 + BPG + 24)
+    table = torch.tensor([[3 + j for j in range(BPG)] for _ in range(1)], dtype=torch.int32, device=cuda)
+    eng.prefill(np.asarray(root, np.uint32), np.array([P], np.int32), kv_pool=pool, kv_block_table=table)
+    oracle = RefModel(cfg, sd, mode=mode)
+    status = torch.full((1,), -1, dtype=torch.int32, device=cuda)
+    path, slots = [], [20 * 16 + 5, 21 * 16 + 0, 20 * 16 + 9, 23 * 16 + 15]
+    for j in range(4):
+        tok = int(rng.integers(0, 1968))
+        extras = np.array([slots[: j + 1]], np.int32)
+        out = eng.extend(np.array([tok]), np.array([P + j], np.int32), [1], np.array([P], np.int32), table, extras,
+                         np.array([j + 1], np.int32), pool, status=status)
+        torch.cuda.synchronize()
+        assert int(status.item()) == 0
+        path.append(tok)
+        ref = oracle.forward_last([np.asarray(root + path, np.int64)])
+        check(out, ref, 2e-2, f"{mode} leaf {j}")
+    eng.close()
+
+
 # (prefix lengths, level-1 children per root): one root of 70 children spans
 # two 64-query tiles of the tree kernel; groups of at most 16 children over
 # prefix tables of at most 8 chunks take the split-prefix kernels in bf16
