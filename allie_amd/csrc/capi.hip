@@ -145,6 +145,7 @@ struct allie_model {
   // forked from and joined back into the caller's stream by the events
   hipStream_t side[2] = {nullptr, nullptr};
   hipEvent_t fork = nullptr, join[2] = {nullptr, nullptr};
+  int64_t split_tokens = 24576;  // 0: never split (allie_model_set_split_tokens)
 };
 
 namespace {
@@ -639,10 +640,12 @@ ExtendWS layout_extend(const allie_model* m, int n, int G, char* base, bool with
   return w;
 }
 
-// A bf16 prefill of at least this many tokens (and no KV pool or status
-// output) runs as two halves on two streams; so does an extend of as many
-// tokens in groups of several tokens each
-constexpr int64_t PREFILL_SPLIT_TOKENS = 24576;
+// A bf16 prefill of at least m->split_tokens tokens (and no KV pool or
+// status output) runs as two halves on two streams; so does an extend of as
+// many tokens in groups of several tokens each
+bool split_size(const allie_model* m, int64_t tokens) {
+  return m->act_bf16 && m->split_tokens > 0 && tokens >= m->split_tokens;
+}
 
 // *out = *a | *b (the validation flags of an extend's two halves)
 __global__ void or_status_kernel(int32_t* out, const int32_t* a, const int32_t* b) {
@@ -964,6 +967,13 @@ int allie_model_set_weight_fp8(allie_model* m, int kind, int layer, const uint8_
   return ALLIE_OK;
 }
 
+int allie_model_set_split_tokens(allie_model* m, int64_t tokens) {
+  if (!m) return fail(ALLIE_ERR_ARG, "null model");
+  if (tokens < 0) return fail(ALLIE_ERR_ARG, "split threshold %lld < 0", (long long)tokens);
+  m->split_tokens = tokens;
+  return ALLIE_OK;
+}
+
 int allie_model_finalize(allie_model* m) {
   if (!m) return fail(ALLIE_ERR_ARG, "model is NULL");
   for (int k = ALLIE_W_WTE; k <= ALLIE_W_TIME_B; ++k)
@@ -1019,7 +1029,7 @@ size_t allie_prefill_workspace_bytes(const allie_model* m, int n_seq, int n_toke
   // a prefill that runs as two halves needs a second copy of the per-game
   // and fixed parts and the alignment of the second half's arrays (a smaller
   // workspace runs it in one piece)
-  if (m->act_bf16 && n_tokens >= PREFILL_SPLIT_TOKENS && n_seq >= 2)
+  if (split_size(m, n_tokens) && n_seq >= 2)
     b += layout_prefill(m, n_seq, 0, nullptr).total + 32 * 256;
   return b;
 }
@@ -1063,7 +1073,7 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
   // each half computes exactly what the whole batch would for its games.
   int cut = 0;
   int64_t T0 = 0;
-  if (m->act_bf16 && !kv_pool && !status && T >= PREFILL_SPLIT_TOKENS && n_seq >= 2) {
+  if (split_size(m, T) && !kv_pool && !status && n_seq >= 2) {
     int64_t acc = 0;
     for (int i = 0; i < n_seq - 1; ++i) {
       acc += lens_host[i] < max_len ? lens_host[i] : max_len;
@@ -1121,7 +1131,7 @@ size_t allie_extend_workspace_bytes(const allie_model* m, int n_tok, int n_group
   if (!m || n_tok < 0 || n_groups < 0) return 0;
   size_t b = layout_extend(m, n_tok, n_groups, nullptr, true).total;
   // room for the two halves of a split extend (see allie_prefill_workspace_bytes)
-  if (m->act_bf16 && n_tok >= PREFILL_SPLIT_TOKENS && n_groups >= 2)
+  if (split_size(m, n_tok) && n_groups >= 2)
     b += layout_extend(m, 0, n_groups, nullptr, true).total + 32 * 256;
   return b;
 }
@@ -1331,7 +1341,7 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   // A large extend of multi-token groups (MCTS tree levels) runs as two halves
   // of consecutive groups on the model's two streams, as a large prefill does:
   // groups never share keys they write, and each reads only its own prefix.
-  if (m->act_bf16 && plan.n1 == 0 && n_tok >= PREFILL_SPLIT_TOKENS && n_groups >= 2 && m->fork) {
+  if (split_size(m, n_tok) && plan.n1 == 0 && n_groups >= 2 && m->fork) {
     int gc = 1;
     while (gc < n_groups - 1 && 2 * (int64_t)group_start_host[gc] < n_tok) ++gc;
     const int t0 = group_start_host[gc];

@@ -467,6 +467,12 @@ def bench_c3(args):
         t, attn = run_tree(probe_levels=(1, 2, 4))
         level_ms += np.array(t)
     level_ms /= args.steps
+    # the same tree with every level in one piece (no two-stream split), for
+    # level 4's attention on its own: in two halves its launches share the
+    # GPU with the other half's GEMMs
+    eng.set_split_tokens(0)
+    t1, attn1 = run_tree(probe_levels=(4,))
+    eng.set_split_tokens(24576)
     d, L, P = cfg.d_model, cfg.n_layer, lay.prefix_len
     kv_tok = 2 * d * 2  # bytes of one token's keys + values, one layer
     roof = {}
@@ -486,6 +492,11 @@ def bench_c3(args):
     fl4 = 4 * d * n4 * (P + 4)  # QK^T and PV over each node's P + 4 keys
     roof[4].update(unique_bytes_per_layer=uniq, achieved_unique_GBs=uniq / (roof[4]["ms_per_layer"] * 1e-3) / 1e9,
                    alg_flop_per_layer=fl4, achieved_TFLOPs=fl4 / (roof[4]["ms_per_layer"] * 1e-3) / 1e12)
+    tot1, cnt1, span1 = attn1[4]
+    roof[4]["one_piece"] = {"note": "the same level in one piece on one stream (split threshold 0)",
+                            "level_ms": t1[3], "ms_per_layer": span1 / L, "avg_launch_ms": tot1 / max(cnt1, 1),
+                            "achieved_TFLOPs": fl4 / (span1 / L * 1e-3) / 1e12,
+                            "achieved_unique_GBs": uniq / (span1 / L * 1e-3) / 1e9}
     total_ms = float(level_ms.sum())
     leaves = lay.level_size(lay.depth)
     flops = sum(2 * cfg.linear_params * lay.level_size(k) + 4 * d * L * lay.level_size(k) * (P + k)

@@ -102,6 +102,13 @@ int allie_model_set_weight_fp8(allie_model* m, int kind, int layer, const uint8_
                                void* stream);
 /* Checks that every weight was set; required before any forward call. */
 int allie_model_finalize(allie_model* m);
+/* Threshold of the two-stream split (bf16 modes): a prefill, or an extend of
+ * groups of several tokens, of at least `tokens` tokens runs as two halves on
+ * two streams of the model's own (see allie_prefill and allie_extend); 0
+ * turns the split off.  Default 24,576.  No reference counterpart: a tuning
+ * knob for callers that run their own streams.  Workspace sizes reported
+ * afterwards follow the new threshold. */
+int allie_model_set_split_tokens(allie_model* m, int64_t tokens);
 
 /* Ragged packing (replaces the padding half of pad_and_collate,
  * src/modeling/data.py:281-337, for a flat word stream).
@@ -154,7 +161,8 @@ typedef struct allie_outputs {
  * allie_pack_ragged): 4 a game longer than its kv_block_table row (its tail
  * is not cached), 8 the <PAD> id inside a game (the reference's padded batch
  * would mask that token, data.py:321; here it is an ordinary token).
- * A bf16 prefill of at least 24,576 tokens with neither kv_pool nor status
+ * A bf16 prefill of at least 24,576 tokens (allie_model_set_split_tokens)
+ * with neither kv_pool nor status
  * runs as two halves of consecutive games on two streams of its own, forked
  * from and joined back into `stream` (results as for one piece: rows never
  * interact across games); it needs the workspace that
