@@ -81,14 +81,17 @@ def executed_flops(cfg, lens):
     return full - gemm_skip - attn_skip
 
 
-def read_traffic(key: str = ""):
+def read_traffic(key: str = "", one_piece: bool = False):
     """HBM bytes per launch of a dominant kernel, measured with rocprofv3
     --pmc FETCH_SIZE / WRITE_SIZE and scaled by the copy calibration: the
     line ``hbm_bytes_per_launch: N`` of the fc GEMM's committed summary, or
-    ``hbm_bytes_per_launch[key]: N`` of the attention kernels' one; None when
-    the summary is absent."""
+    ``hbm_bytes_per_launch[key]: N`` of the attention kernels' one, or (with
+    one_piece) the fc GEMM's launch over the whole batch in one piece; None
+    when the summary is absent."""
     path = TRAFFIC_FILE if not key else ATTN_TRAFFIC_FILE
     tag = "hbm_bytes_per_launch:" if not key else f"hbm_bytes_per_launch[{key}]:"
+    if one_piece:
+        tag = "hbm_bytes_per_launch_one_piece:"
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -326,7 +329,8 @@ def run_prefill(args, cfg, mode, workload):
         "launch_span_ms": fc_span / args.steps, "launch_sum_ms": fc_tot / args.steps,
         "one_piece": {"note": "the same forward with the batch in one piece on one stream",
                       "avg_launch_ms": iso_tot / max(iso_n, 1), "launches": iso_n, "achieved": iso_tflops,
-                      "frac": iso_tflops / MFMA_BF16_PEAK_TFLOPS},
+                      "frac": iso_tflops / MFMA_BF16_PEAK_TFLOPS,
+                      "traffic": read_traffic(one_piece=True) if (mode == "bfloat16" and cfg.d_model == 1024) else None},
     }
     return res, eng, sd, seqs, lens, words, out
 
@@ -516,6 +520,7 @@ def bench_c3(args):
                        "traffic_measured_on": traffic_commit("c3_level1"),
                        "level2": dict(roof[2], traffic=read_traffic("c3_level2")),
                        "level4": dict(roof[4], traffic=read_traffic("c3_level4"))}
+    res["roofline"]["level4"]["one_piece"]["traffic"] = read_traffic("c3_level4_one_piece")
     eng.close()
     res["cpu_baseline"] = None
     if not args.no_cpu_baseline:
