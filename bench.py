@@ -496,6 +496,9 @@ def bench_c3(args):
     fl4 = 4 * d * n4 * (P + 4)  # QK^T and PV over each node's P + 4 keys
     roof[4].update(unique_bytes_per_layer=uniq, achieved_unique_GBs=uniq / (roof[4]["ms_per_layer"] * 1e-3) / 1e9,
                    alg_flop_per_layer=fl4, achieved_TFLOPs=fl4 / (roof[4]["ms_per_layer"] * 1e-3) / 1e12)
+    roof[4]["note"] = ("the level runs as two halves on two streams: each half's attention launch runs beside the "
+                       "other half's GEMMs, at a different time from the other's, so ms_per_layer is the union of "
+                       "two launches that share the GPU; one_piece times the attention alone")
     tot1, cnt1, span1 = attn1[4]
     roof[4]["one_piece"] = {"note": "the same level in one piece on one stream (split threshold 0)",
                             "level_ms": t1[3], "ms_per_layer": span1 / L, "avg_launch_ms": tot1 / max(cnt1, 1),
