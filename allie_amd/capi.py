@@ -51,7 +51,7 @@ _SIGS = [
     ("allie_model_set_weight_fp8", C.c_int,
      [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_void_p]),
     ("allie_model_finalize", C.c_int, [C.c_void_p]),
-    ("allie_model_set_split_tokens", C.c_int, [C.c_void_p, C.c_int64]),
+    ("allie_model_set_split_tokens", C.c_int, [C.c_void_p, C.c_int64, C.c_int64]),
     ("allie_pack_ragged", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
       C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,

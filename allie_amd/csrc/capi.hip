@@ -145,7 +145,9 @@ struct allie_model {
   // forked from and joined back into the caller's stream by the events
   hipStream_t side[2] = {nullptr, nullptr};
   hipEvent_t fork = nullptr, join[2] = {nullptr, nullptr};
-  int64_t split_tokens = 24576;  // 0: never split (allie_model_set_split_tokens)
+  // two-stream split thresholds (allie_model_set_split_tokens; 0: never)
+  int64_t split_tokens = 24576;  // a prefill's tokens, an extend's tokens
+  int64_t split_decode = 512;    // an extend's one-token groups (decode steps)
 };
 
 namespace {
@@ -642,9 +644,12 @@ ExtendWS layout_extend(const allie_model* m, int n, int G, char* base, bool with
 
 // A bf16 prefill of at least m->split_tokens tokens (and no KV pool or
 // status output) runs as two halves on two streams; so does an extend of as
-// many tokens in groups of several tokens each
+// many tokens, or of at least m->split_decode one-token groups (decode steps)
 bool split_size(const allie_model* m, int64_t tokens) {
   return m->act_bf16 && m->split_tokens > 0 && tokens >= m->split_tokens;
+}
+bool split_decode_size(const allie_model* m, int64_t one_token_groups) {
+  return m->act_bf16 && m->split_decode > 0 && one_token_groups >= m->split_decode;
 }
 
 // *out = *a | *b (the validation flags of an extend's two halves)
@@ -967,10 +972,12 @@ int allie_model_set_weight_fp8(allie_model* m, int kind, int layer, const uint8_
   return ALLIE_OK;
 }
 
-int allie_model_set_split_tokens(allie_model* m, int64_t tokens) {
+int allie_model_set_split_tokens(allie_model* m, int64_t tokens, int64_t decode_tokens) {
   if (!m) return fail(ALLIE_ERR_ARG, "null model");
-  if (tokens < 0) return fail(ALLIE_ERR_ARG, "split threshold %lld < 0", (long long)tokens);
+  if (tokens < 0 || decode_tokens < 0)
+    return fail(ALLIE_ERR_ARG, "split thresholds %lld, %lld < 0", (long long)tokens, (long long)decode_tokens);
   m->split_tokens = tokens;
+  m->split_decode = decode_tokens;
   return ALLIE_OK;
 }
 
@@ -1131,7 +1138,7 @@ size_t allie_extend_workspace_bytes(const allie_model* m, int n_tok, int n_group
   if (!m || n_tok < 0 || n_groups < 0) return 0;
   size_t b = layout_extend(m, n_tok, n_groups, nullptr, true).total;
   // room for the two halves of a split extend (see allie_prefill_workspace_bytes)
-  if (split_size(m, n_tok) && n_groups >= 2)
+  if ((split_size(m, n_tok) || split_decode_size(m, n_tok)) && n_groups >= 2)
     b += layout_extend(m, 0, n_groups, nullptr, true).total + 32 * 256;
   return b;
 }
@@ -1338,10 +1345,12 @@ int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_t
   if (!workspace) return fail(ALLIE_ERR_ARG, "bad extend arguments");
   ExtendWS w = layout_extend(m, n_tok, n_groups, (char*)workspace, true);
   hipStream_t st = (hipStream_t)stream;
-  // A large extend of multi-token groups (MCTS tree levels) runs as two halves
-  // of consecutive groups on the model's two streams, as a large prefill does:
-  // groups never share keys they write, and each reads only its own prefix.
-  if (split_size(m, n_tok) && plan.n1 == 0 && n_groups >= 2 && m->fork) {
+  // A large extend (MCTS tree levels; or a decode step of many games, whose
+  // HBM-bound attention then runs beside the other half's latency-bound
+  // projections) runs as two halves of consecutive groups on the model's two
+  // streams, as a large prefill does: groups never share keys they write, and
+  // each reads only its own prefix.
+  if ((split_size(m, n_tok) || split_decode_size(m, plan.n1)) && n_groups >= 2 && m->fork) {
     int gc = 1;
     while (gc < n_groups - 1 && 2 * (int64_t)group_start_host[gc] < n_tok) ++gc;
     const int t0 = group_start_host[gc];

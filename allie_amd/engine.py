@@ -290,11 +290,12 @@ class Engine:
             capi.ptr(kv_pool), self.pool_blocks(kv_pool), capi.ptr(status), capi.stream_ptr())
         capi.check(rc, "allie_extend_noalloc")
 
-    def set_split_tokens(self, tokens: int) -> None:
-        """Threshold of the two-stream split of large bf16 prefills and
-        extends (``allie_model_set_split_tokens``); 0 runs every batch in one
-        piece."""
-        capi.check(self._lib.allie_model_set_split_tokens(self._m, int(tokens)), "allie_model_set_split_tokens")
+    def set_split_tokens(self, tokens: int, decode_tokens: int = 512) -> None:
+        """Thresholds of the two-stream split of large bf16 prefills and
+        extends, and of extends with many one-token groups
+        (``allie_model_set_split_tokens``); 0 turns a split off."""
+        capi.check(self._lib.allie_model_set_split_tokens(self._m, int(tokens), int(decode_tokens)),
+                   "allie_model_set_split_tokens")
 
     def close(self) -> None:
         if getattr(self, "_m", None):

@@ -474,9 +474,9 @@ def bench_c3(args):
     # the same tree with every level in one piece (no two-stream split), for
     # level 4's attention on its own: in two halves its launches share the
     # GPU with the other half's GEMMs
-    eng.set_split_tokens(0)
+    eng.set_split_tokens(0, 0)
     t1, attn1 = run_tree(probe_levels=(4,))
-    eng.set_split_tokens(24576)
+    eng.set_split_tokens(24576, 512)
     d, L, P = cfg.d_model, cfg.n_layer, lay.prefix_len
     kv_tok = 2 * d * 2  # bytes of one token's keys + values, one layer
     roof = {}
@@ -555,7 +555,8 @@ def bench_c4(args):
     assert int(cb.status.item()) == 0, "extend status"
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     probed = args.steps  # every decode attention launch of the timed steps is timed
-    probe = Probe(capi.PROBE_DECODE, probed * cfg.n_layer)
+    # a step of many games runs as two halves on two streams: two launches per layer
+    probe = Probe(capi.PROBE_DECODE, 2 * probed * cfg.n_layer)
     tok0, keys0 = cb.tokens, cb.keys_read
     keys_probed = dec_probed = 0
     t0 = time.perf_counter()
@@ -569,29 +570,61 @@ def bench_c4(args):
         evs[i + 1].record()
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
+    att_span = probe.span()
     att_tot, att_n = probe.end()
     lat = np.array([evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)])
     ms = el * 1000.0 / args.steps
     appended = cb.tokens - tok0
     tok_s = appended / el
+    mean_keys = (cb.keys_read - keys0) / args.steps
+    games_started = cb.games_started
+    # the same self-play continued with every step in one piece (decode split
+    # off), for the attention kernel on its own
+    n1 = max(args.steps // 10, 20)
+    eng.set_split_tokens(24576, 0)
+    probe1 = Probe(capi.PROBE_DECODE, 2 * n1 * cfg.n_layer)
+    k1, dd1 = cb.decode_keys, cb.decoded
+    for _ in range(n1):
+        cb.step()
+    torch.cuda.synchronize()
+    span1 = probe1.span()
+    tot1, cnt1 = probe1.end()
+    k1, dd1 = cb.decode_keys - k1, cb.decoded - dd1
+    eng.set_split_tokens(24576, 512)
     d = cfg.d_model
     att_ms = att_tot / max(att_n, 1)
-    # per decode-attention launch (one layer): the running games' keys and
-    # values read (all heads), their queries read and outputs written
+    # per layer of a step: the running games' keys and values read (all
+    # heads), their queries read and outputs written; over the time during
+    # which a decode-attention launch of that layer ran (the union of the
+    # launches' intervals: one launch, or one per half)
     att_bytes = (keys_probed / probed) * 2 * d * 2 + (dec_probed / probed) * 2 * d * 2
-    achieved = att_bytes / (att_ms * 1e-3) / 1e9
+    layer_ms = att_span / (probed * cfg.n_layer)
+    achieved = att_bytes / (layer_ms * 1e-3) / 1e9
+    bytes1 = (k1 / n1) * 2 * d * 2 + (dd1 / n1) * 2 * d * 2
+    layer1_ms = span1 / (n1 * cfg.n_layer)
+    achieved1 = bytes1 / (layer1_ms * 1e-3) / 1e9
     res = base_result(args, tok_s, "tokens/s", ms, "bf16",
                       f"C4 continuous-batching self-play decode: medium bf16, {cb.S} slots, prefixes U[1,50], "
                       "game length Geometric(mean 80) capped 512, greedy argmax, refill on finish",
                       step_ms_p50=float(np.percentile(lat, 50)), step_ms_p90=float(np.percentile(lat, 90)),
                       step_ms_p99=float(np.percentile(lat, 99)),
-                      mean_keys_per_step=(cb.keys_read - keys0) / args.steps,
-                      moves_appended=appended, games_started=cb.games_started)
+                      mean_keys_per_step=mean_keys,
+                      moves_appended=appended, games_started=games_started)
     res["roofline"] = {"kernel": "attn_extend_wave_kernel (decode: one token per running game over its paged KV)",
                        "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic("c4_decode"),
-                       "traffic_measured_on": traffic_commit("c4_decode"), "avg_launch_ms": att_ms,
-                       "alg_bytes_per_launch": att_bytes}
+                       "traffic_measured_on": traffic_commit("c4_decode"),
+                       "achieved_is": "decode-attention bytes of a layer / the time during which that layer's "
+                                      "attention launches ran (two per layer when the step runs as two halves, "
+                                      "each beside the other half's projections)",
+                       "alg_bytes_per_layer": att_bytes, "ms_per_layer": layer_ms, "avg_launch_ms": att_ms,
+                       "launches_per_layer": att_n / (probed * cfg.n_layer),
+                       "one_piece": {"note": f"{n1} more steps of the same self-play, each in one piece on one "
+                                             "stream (decode split threshold 0)",
+                                     "ms_per_layer": layer1_ms, "alg_bytes_per_layer": bytes1,
+                                     "achieved": achieved1, "frac": achieved1 / HBM_PEAK_GBS,
+                                     "traffic": read_traffic("c4_decode_one_piece"),
+                                     "launches_per_layer": cnt1 / (n1 * cfg.n_layer)}}
     eng.close()
     res["cpu_baseline"] = None
     if not args.no_cpu_baseline:

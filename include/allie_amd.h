@@ -102,13 +102,14 @@ int allie_model_set_weight_fp8(allie_model* m, int kind, int layer, const uint8_
                                void* stream);
 /* Checks that every weight was set; required before any forward call. */
 int allie_model_finalize(allie_model* m);
-/* Threshold of the two-stream split (bf16 modes): a prefill, or an extend of
- * groups of several tokens, of at least `tokens` tokens runs as two halves on
- * two streams of the model's own (see allie_prefill and allie_extend); 0
- * turns the split off.  Default 24,576.  No reference counterpart: a tuning
- * knob for callers that run their own streams.  Workspace sizes reported
- * afterwards follow the new threshold. */
-int allie_model_set_split_tokens(allie_model* m, int64_t tokens);
+/* Thresholds of the two-stream split (bf16 modes): a prefill or an extend of
+ * at least `tokens` tokens, or an extend with at least `decode_tokens`
+ * one-token groups (decode steps), runs as two halves on two streams of the
+ * model's own (see allie_prefill and allie_extend); 0 turns that split off.
+ * Defaults 24,576 and 512.  No reference counterpart: a tuning knob for
+ * callers that run their own streams.  Workspace sizes reported afterwards
+ * follow the new thresholds. */
+int allie_model_set_split_tokens(allie_model* m, int64_t tokens, int64_t decode_tokens);
 
 /* Ragged packing (replaces the padding half of pad_and_collate,
  * src/modeling/data.py:281-337, for a flat word stream).

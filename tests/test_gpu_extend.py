@@ -46,14 +46,18 @@ def tiny():
     return cfg, weights.init_weights(cfg, seed=11, perturb=True)
 
 
-@pytest.mark.parametrize("mode,tol", [("float32", 1e-4), ("bfloat16", 2e-2)])
-def test_decode_steps_match_full_recompute(tiny, mode, tol, cuda):
+@pytest.mark.parametrize("mode,tol,split", [("float32", 1e-4, False), ("bfloat16", 2e-2, False), ("bfloat16", 2e-2, True)])
+def test_decode_steps_match_full_recompute(tiny, mode, tol, split, cuda):
+    """Decode steps of 9 games; with split, the step's one-token groups run as
+    two halves on the model's two streams (threshold lowered to 4 games)."""
     cfg, sd = tiny
     rng = np.random.default_rng(5)
     B = 9
     lens = rng.integers(1, 70, B).astype(np.int32)
     seqs = [list(rng.integers(0, 1968, n)) for n in lens]
     eng = Engine(cfg, sd, mode=mode)
+    if split:
+        eng.set_split_tokens(24576, 4)
     pool = nan_pool(eng, B * BPG + 3)
     # game b owns blocks 3 + b * BPG ...: a non-contiguous, non-zero layout
     table = torch.tensor([[3 + b * BPG + j for j in range(BPG)] for b in range(B)], dtype=torch.int32, device=cuda)

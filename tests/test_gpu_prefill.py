@@ -113,9 +113,9 @@ def test_prefill_two_halves(tiny, mode, cuda):
     one = run_engine(eng, seqs, lens, legal=legal, temperature=0.9,
                      status=torch.zeros(1, dtype=torch.int32, device=cuda))
     # a split threshold of 0 runs the batch in one piece too: the same path
-    eng.set_split_tokens(0)
+    eng.set_split_tokens(0, 0)
     one0 = run_engine(eng, seqs, lens, legal=legal, temperature=0.9)
-    eng.set_split_tokens(24576)
+    eng.set_split_tokens(24576, 512)
     for k in ("logits", "value", "time", "top1"):
         assert np.array_equal(one0[k], one[k]), k
     for b, ids in enumerate(legal_ids):
