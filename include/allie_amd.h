@@ -209,7 +209,12 @@ int allie_prefill(allie_model* m, const uint32_t* words, const int32_t* lens_hos
  * writes the P keys before attention, and token t sees positions 0..t.  A
  * batch may mix such groups with decode steps; one-token groups placed first
  * are streamed by the decode kernel, the rest share their group's keys
- * across query tiles. */
+ * across query tiles.
+ * A bf16 extend of at least 24,576 tokens, or with at least 512 leading
+ * one-token groups (allie_model_set_split_tokens), runs as two halves of
+ * consecutive groups on the model's two streams, forked from and joined back
+ * into `stream`, the halves' flags OR-ed into status; it needs the workspace
+ * that allie_extend_workspace_bytes reports, and runs in one piece on less. */
 size_t allie_extend_workspace_bytes(const allie_model* m, int n_tok, int n_groups);
 int allie_extend(allie_model* m, const int32_t* ids, const int32_t* pos, int n_tok,
                  const int32_t* group_start_host, int n_groups, const int32_t* prefix_len,
