@@ -1343,6 +1343,10 @@ int gemm_split_factor(int M, int N, int K) {
   // K = 1024 projection is fastest unsplit (13 us against 18 us at 2
   // splits) while K = 4096 still gains at 2 (32 us against 46 us)
   const int cap = K >= 2048 ? 256 : 96;
+  // K = 1024 with at least 32 tiles (the attention c_proj of a C4 half-step,
+  // M = 512-750): unsplit 12.1-12.4 us against 12.5-13.8 at the 2 splits the
+  // cap allows (allie_gemm_splitk, 24 weight matrices in turn)
+  if (K < 2048 && tiles >= 32) return 1;
   while (s < 8 && tiles * s * 2 <= cap && KT % (s * 2) == 0 && KT / (s * 2) >= 8) s *= 2;
   return s;
 }

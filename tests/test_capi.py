@@ -95,6 +95,8 @@ def test_gemm_split_factor_of_decode_shapes():
     assert f(1024, 1024, 4096) == 4
     assert f(1450, 1024, 4096) == 2  # C4 step (about 1,450 rows)
     assert f(1450, 3072, 1024) == 1
+    assert f(640, 1024, 1024) == 1   # attention c_proj of a C4 half-step (32+ tiles at K = 1024)
+    assert f(256, 1024, 1024) == 4   # fewer tiles: still split
     for M in (1, 8, 64, 256, 1450, 53205):
         for N, K in ((3072, 1024), (1024, 1024), (4096, 1024), (1024, 4096)):
             s = f(M, N, K)
