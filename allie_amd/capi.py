@@ -52,6 +52,7 @@ _SIGS = [
      [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_void_p]),
     ("allie_model_finalize", C.c_int, [C.c_void_p]),
     ("allie_model_set_split_tokens", C.c_int, [C.c_void_p, C.c_int64, C.c_int64]),
+    ("allie_model_set_tree_heads", C.c_int, [C.c_void_p, C.c_int]),
     ("allie_pack_ragged", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
       C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,

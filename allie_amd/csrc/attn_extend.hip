@@ -528,20 +528,29 @@ constexpr int TREE_EB = 8;  // extra indices per column batch
 // K rows (bf16, 128 B): 16-byte chunk c of row r at c ^ kswz(r)
 ALLIE_DEV int kswz(int r) { return (r >> 1) & 7; }
 
-template <int NW, int DEPTH>
+// MH: the workgroup takes heads h0 .. h0 + hg - 1 (hg = a.head_group) of its
+// tile in turn, with the positions, own slots, block table and columns
+// loaded and built once, and its chunk sequence running on from one head
+// into the next, so the next head's first chunks load while the current
+// head's last are multiplied.  Each head's arithmetic is the one-head
+// kernel's, in the same order (the same bits).  Needs a single column batch
+// (max_extra <= TREE_EB).
+template <int NW, int DEPTH, bool MH>
 __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttnArgs a) {
   constexpr int TQ = NW * 16, NT = NW * 64, PER = 512 / NT;  // PER: 16-byte K (and V) pieces per thread per chunk
   static_assert(NT >= TREE_MAX_BLOCKS, "one thread per staged block id");
   constexpr int NH = TQ / 64;                               // 64-token halves (column builder waves)
   constexpr int MAXC = TQ * TREE_EB;
-  __shared__ __attribute__((aligned(1024))) uint16_t sK[KT * HD];
-  __shared__ __attribute__((aligned(1024))) uint16_t sV[KT * HD];
+  constexpr int NBUF = MH ? 2 : 1;  // LDS chunk buffers (MH: one staged while the other is multiplied)
+  __shared__ __attribute__((aligned(1024))) uint16_t sK[NBUF * KT * HD];
+  __shared__ __attribute__((aligned(1024))) uint16_t sV[NBUF * KT * HD];
   __shared__ int32_t c_slot[MAXC + 64];   // column -> pool slot (-1: padding)
   __shared__ __attribute__((aligned(16))) uint32_t c_rng[MAXC + 64];  // column -> tile-local queries [lo, hi): lo | hi << 16
   __shared__ int32_t s_blk[TREE_MAX_BLOCKS];  // the prefix's pool blocks (-1: skipped)
   __shared__ int32_t s_tot[NH];
 
-  const int head = blockIdx.y;
+  const int hg = MH ? a.head_group : 1;
+  const int h0 = blockIdx.y * hg;
   const int tile = a.tiles[blockIdx.x];
   const int g = tile >> 8, qt = tile & 255;
   const int H = a.n_head, d = H * HD, ld = 3 * d;
@@ -550,7 +559,9 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
   const bf16_t* __restrict__ qkv = reinterpret_cast<const bf16_t*>(a.qkv);
   const bf16_t* __restrict__ pool = reinterpret_cast<const bf16_t*>(a.pool);
   const int64_t voff = (int64_t)H * KV_BLOCK * HD;  // k -> v of the same (block, layer, head)
-  const bf16_t* lbase = pool + ((int64_t)a.layer * a.pool_blocks * 2 * H + head) * (KV_BLOCK * HD);
+  // pool base of head h0 + hh at this layer
+  const bf16_t* lbase0 = pool + ((int64_t)a.layer * a.pool_blocks * 2 * H + h0) * (KV_BLOCK * HD);
+  auto hbase = [&](int hh) { return lbase0 + (int64_t)hh * (KV_BLOCK * HD); };
   const int64_t bstride = (int64_t)2 * H * KV_BLOCK * HD;
   const int q_first = a.group_start[g] + qt * TQ;
   const int ntok = min(TQ, a.group_start[g + 1] - q_first);
@@ -575,9 +586,12 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
   const int pos_qi = a.pos[qi];
   const int self_v = a.self_slot[qi];
   bf16x8_t qf[2];  // B operand of S^T = K Q^T: query lq, dims 32 ks + 8 lg .. +7
+  auto load_q = [&](int head) {
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
-    qf[ks] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(qkv + (int64_t)qi * ld + head * HD + 32 * ks + 8 * lg));
+    for (int ks = 0; ks < 2; ++ks)
+      qf[ks] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(qkv + (int64_t)qi * ld + head * HD + 32 * ks + 8 * lg));
+  };
+  load_q(h0);
   if (tid < TREE_MAX_BLOCKS) s_blk[tid] = (tid < nbp && tid < a.max_blocks) ? valid_blk(bt_v) : -1;
   const int lim = q_ok ? min(P, pos_qi) : 0;
 
@@ -644,17 +658,21 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
   };
 
   const float c2 = a.scale * 1.4426950408889634f;
-  float m_run = -INFINITY, l_run = 0.f;
-  f32x4_t o[4] = {f32x4_t{}, f32x4_t{}, f32x4_t{}, f32x4_t{}};  // O^T: dims 16 db + 4 lg .. +3 of query lq
-  {
-    // The token's own key and value (its last private key) are read from its
-    // slot by its own lanes: the softmax starts from that key, and the
-    // columns carry only the other private keys (a tree level's own keys
-    // would otherwise be one column per query).
-    // (self_slot: the prepare step's copy, one dependent load instead of two)
-    const int sl = (q_ok && self_v >= 0 && (self_v >> 4) < a.pool_blocks) ? self_v : -1;
-    const bool has_self = sl >= 0;
-    const bf16_t* row = lbase + (int64_t)(has_self ? sl >> 4 : 0) * bstride + (sl & 15) * HD;
+  float m_run, l_run;
+  f32x4_t o[4];  // O^T: dims 16 db + 4 lg .. +3 of query lq
+  // A head's softmax opens with the token's own key and value (its last
+  // private key), read from its slot by its own lanes; the columns carry only
+  // the other private keys (a tree level's own keys would otherwise be one
+  // column per query).  (self_slot: the prepare step's copy, one dependent
+  // load instead of two.)  Needs the head's queries in qf.
+  const int self_sl = (q_ok && self_v >= 0 && (self_v >> 4) < a.pool_blocks) ? self_v : -1;
+  auto open_head = [&](int hh) {
+    m_run = -INFINITY;
+    l_run = 0.f;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[db] = f32x4_t{};
+    const bool has_self = self_sl >= 0;
+    const bf16_t* row = hbase(hh) + (int64_t)(has_self ? self_sl >> 4 : 0) * bstride + (self_sl & 15) * HD;
     float sdot = 0.f;
     uint2 vs[4] = {};
     if (has_self) {
@@ -679,15 +697,31 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
       for (int db = 0; db < 4; ++db)
         o[db] = f32x4_t{bf2f(vs[db].x & 0xffffu), bf2f(vs[db].x >> 16), bf2f(vs[db].y & 0xffffu), bf2f(vs[db].y >> 16)};
     }
-  }
+  };
+  // normalise and store head h0 + hh's output rows (no barriers)
+  auto close_head = [&](int hh) {
+    if (!q_ok) return;
+    const float l_tot = xor32_sum(xor16_sum(l_run));
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    bf16_t* out = reinterpret_cast<bf16_t*>(a.out) + (int64_t)qi * d + (h0 + hh) * HD + 4 * lg;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      uint2 w;
+      w.x = pack_bf16x2(o[db][0] * inv, o[db][1] * inv);
+      w.y = pack_bf16x2(o[db][2] * inv, o[db][3] * inv);
+      *reinterpret_cast<uint2*>(out + 16 * db) = w;
+    }
+  };
+  open_head(0);
   const bool wave_busy = wave * 16 < ntok;  // a wave past the tile's tokens only stages keys
   const int trow = lq >> 2, tchunk = lq & 3;  // transposing read: key row within 4, 4-dim chunk
   const int nchp = (P + KT - 1) / KT;
 
-  // chunk j (prefix chunks first, then columns from c_slot) into registers:
-  // this thread's piece it is key row (tid + NT it) / 8, 16-byte chunk % 8;
-  // a key outside a kept block reads block 0 and is zeroed at staging
-  auto fetch = [&](int j, int ncp, uint4 (&kv)[PER], uint4 (&vv)[PER], bool (&okf)[PER]) {
+  // chunk j (prefix chunks first, then columns from c_slot) of the head whose
+  // pool base is hb into registers: this thread's piece it is key row
+  // (tid + NT it) / 8, 16-byte chunk % 8; a key outside a kept block reads
+  // block 0 and is zeroed at staging
+  auto fetch = [&](const bf16_t* hb, int j, int ncp, uint4 (&kv)[PER], uint4 (&vv)[PER], bool (&okf)[PER]) {
 #pragma unroll
     for (int it = 0; it < PER; ++it) {
       const int cidx = tid + NT * it;
@@ -703,44 +737,62 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
         off = sl & 15;
       }
       okf[it] = blk >= 0;
-      const bf16_t* src = lbase + (int64_t)max(blk, 0) * bstride + off * HD + c * 8;
+      const bf16_t* src = hb + (int64_t)max(blk, 0) * bstride + off * HD + c * 8;
       kv[it] = *reinterpret_cast<const uint4*>(src);
       vv[it] = *reinterpret_cast<const uint4*>(src + voff);
     }
   };
-  auto stage = [&](const uint4 (&kv)[PER], const uint4 (&vv)[PER], const bool (&okf)[PER]) {
+  auto stage = [&](const uint4 (&kv)[PER], const uint4 (&vv)[PER], const bool (&okf)[PER], int buf = 0) {
 #pragma unroll
     for (int it = 0; it < PER; ++it) {
       const int cidx = tid + NT * it;
       const int key = cidx >> 3, c = cidx & 7;
       const uint4 k4 = okf[it] ? kv[it] : make_uint4(0, 0, 0, 0);
       const uint4 v4 = okf[it] ? vv[it] : make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4*>(sK + key * HD + ((c ^ kswz(key)) << 3)) = k4;
-      *reinterpret_cast<uint4*>(sV + key * HD + ((c ^ (((key >> 1) & 1) << 1)) << 3)) = v4;
+      *reinterpret_cast<uint4*>(sK + buf * KT * HD + key * HD + ((c ^ kswz(key)) << 3)) = k4;
+      *reinterpret_cast<uint4*>(sV + buf * KT * HD + key * HD + ((c ^ (((key >> 1) & 1) << 1)) << 3)) = v4;
     }
   };
-  auto compute = [&](int j, int ncp) {
+  // LDS read addresses, fixed for every chunk: K row 16 kb + lq, 16-byte
+  // chunk 4 ks + lg, whose swizzle (lq >> 1) & 7 does not depend on kb; V
+  // rows 32 s2 + 16 h + 4 lg + trow read transposed at 4-dim chunk
+  // 4 (db ^ vb) + tchunk, vb = (trow >> 1) & 1 (the row swizzle bit)
+  const int ksw = (lq >> 1) & 7, vb = (trow >> 1) & 1;
+  const uint16_t* kp0 = sK + lq * HD + ((lg ^ ksw) << 3);
+  const uint16_t* kp1 = sK + lq * HD + (((4 + lg) ^ ksw) << 3);
+  const uint16_t* vp = sV + (4 * lg + trow) * HD + 4 * tchunk;
+  const uint16_t* vp0 = vp + 16 * vb;        // db even
+  const uint16_t* vp1 = vp + 16 * (1 - vb);  // db odd
+  // the lowest limit over the wave's queries: a prefix chunk of kept blocks
+  // wholly below it needs no mask
+  int lim_w = lim;
+#pragma unroll
+  for (int sh = 1; sh < 64; sh <<= 1) lim_w = min(lim_w, __shfl_xor(lim_w, sh, 64));
+  lim_w = __builtin_amdgcn_readfirstlane(lim_w);
+  auto compute = [&](int j, int ncp, int buf = 0) {
     // S^T = K Q^T: st[kb][r] is key 16 kb + 4 lg + r of query lq
     f32x4_t st[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       st[kb] = f32x4_t{};
-      const int row = 16 * kb + lq;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8_t kf = __builtin_bit_cast(
-            bf16x8_t, *reinterpret_cast<const u32x4_t*>(sK + row * HD + (((4 * ks + lg) ^ kswz(row)) << 3)));
+        const bf16x8_t kf =
+            __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>((ks ? kp1 : kp0) + buf * KT * HD + kb * 16 * HD));
         st[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], st[kb], 0, 0, 0);
       }
     }
     if (j < ncp) {  // prefix: positions below the query's limit in a kept block
       const int k0 = j * KT;
+      bool bok[4];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        const bool bok = pblk((k0 >> 4) + kb) >= 0;
+      for (int kb = 0; kb < 4; ++kb) bok[kb] = pblk((k0 >> 4) + kb) >= 0;
+      if (!(k0 + KT <= lim_w && bok[0] && bok[1] && bok[2] && bok[3])) {  // uniform
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (!bok || k0 + 16 * kb + 4 * lg + r >= lim) st[kb][r] = -INFINITY;
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (!bok[kb] || k0 + 16 * kb + 4 * lg + r >= lim) st[kb][r] = -INFINITY;
       }
     } else {  // columns: visible to their run of queries
       const int cb = (j - ncp) * 64;
@@ -762,7 +814,7 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
     const float m_new = fmaxf(m_run, mx);
     u32x4_t pf[2];  // P^T of k-step s: keys 32 s + 4 lg + {0..3}, then 32 s + 16 + 4 lg + {0..3}
     if (m_new != -INFINITY) {  // uniform per query
-      const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c2);
+      const float m_old = m_run;
       m_run = m_new;
       const float mc = m_new * c2;
       float p[4][4];
@@ -778,9 +830,16 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
       for (int s2 = 0; s2 < 2; ++s2)
         pf[s2] = u32x4_t{pack_bf16x2(p[2 * s2][0], p[2 * s2][1]), pack_bf16x2(p[2 * s2][2], p[2 * s2][3]),
                          pack_bf16x2(p[2 * s2 + 1][0], p[2 * s2 + 1][1]), pack_bf16x2(p[2 * s2 + 1][2], p[2 * s2 + 1][3])};
-      l_run = l_run * alpha + ls;
+      // a query whose maximum did not move has alpha = exp2(0) = 1 exactly:
+      // when no query of the wave moved, the rescale is skipped (same bits)
+      if (__builtin_amdgcn_ballot_w64(m_new != m_old)) {
+        const float alpha = __builtin_amdgcn_exp2f((m_old - m_new) * c2);
+        l_run = l_run * alpha + ls;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) o[db] *= alpha;
+        for (int db = 0; db < 4; ++db) o[db] *= alpha;
+      } else {
+        l_run = l_run + ls;
+      }
     } else {
       pf[0] = pf[1] = u32x4_t{0, 0, 0, 0};
     }
@@ -790,12 +849,11 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const int r0 = 32 * s2 + 4 * lg + trow, r1 = r0 + 16;
-        const int jj = 4 * db + tchunk;
+        const uint16_t* vr = (db & 1 ? vp1 : vp0) + buf * KT * HD + 32 * s2 * HD + 16 * (db & 2);
         const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-            (lds_bf16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r0 * HD + ((jj ^ (((r0 >> 1) & 1) << 2)) << 2)));
+            (lds_bf16x4_t*)((__attribute__((address_space(3))) uint16_t*)vr));
         const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-            (lds_bf16x4_t*)((__attribute__((address_space(3))) uint16_t*)sV + r1 * HD + ((jj ^ (((r1 >> 1) & 1) << 2)) << 2)));
+            (lds_bf16x4_t*)((__attribute__((address_space(3))) uint16_t*)(vr + 16 * HD)));
         const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
         o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, u32x4_t{l2.x, l2.y, h2.x, h2.y}),
                                                         __builtin_bit_cast(bf16x8_t, pf[s2]), o[db], 0, 0, 0);
@@ -807,51 +865,118 @@ __global__ __launch_bounds__(NW * 64, 4) void attn_extend_tree_kernel(ExtendAttn
   // unconditional (past the last chunk it re-reads the last, never staged):
   // a load under a condition makes the compiler's wait before the next
   // multiply cover the chunk just requested
-  uint4 kA[PER], vA[PER], kB[PER], vB[PER];
-  bool oA[PER], oB[PER];
+  uint4 kA[PER] = {}, vA[PER] = {}, kB[PER] = {}, vB[PER] = {};
+  bool oA[PER] = {}, oB[PER] = {};
   __syncthreads();  // s_blk is in
-  if (nchp > 0) fetch(0, nchp, kA, vA, oA);  // the prefix's first chunks load while the columns are built
-  if (DEPTH > 1 && nchp > 1) fetch(1, nchp, kB, vB, oB);
-  for (int eb = 0; eb < a.max_extra || eb == 0; eb += TREE_EB) {
-    const int ncols = build_columns(eb);
-    const int ncp = eb == 0 ? nchp : 0;  // prefix chunks go with the first batch
-    const int nch = ncp + (ncols + 63) / 64;
-    if (ncp < 1 && nch > 0) fetch(0, ncp, kA, vA, oA);
+  if (nchp > 0) fetch(hbase(0), 0, nchp, kA, vA, oA);  // the prefix's first chunks load while the columns are built
+  if (DEPTH > 1 && nchp > 1) fetch(hbase(0), 1, nchp, kB, vB, oB);
+  if constexpr (MH) {
+    // one column batch; the flat chunk sequence J runs over the heads: head
+    // J / nch, its chunk J % nch
+    const int ncols = build_columns(0);
+    const int nch = nchp + (ncols + 63) / 64;
+    const int NJ = nch * hg;
+    // (only for 0 <= J < NJ, so nch > 0 and the head is one of the group's)
+    auto fetchJ = [&](int J, uint4 (&kv)[PER], uint4 (&vv)[PER], bool (&okf)[PER]) {
+      const int hh = J / nch;
+      fetch(hbase(hh), J - hh * nch, nchp, kv, vv, okf);
+    };
+    if (nchp < 1 && NJ > 0) fetchJ(0, kA, vA, oA);
+    if (DEPTH > 1 && nchp < 2 && NJ > 1) fetchJ(1, kB, vB, oB);
+    int cur = 0;  // the head being multiplied (busy waves)
+    // at the first chunk of the next head: the current head's rows out, the
+    // next head's queries and own key in (before the chunk fetch that
+    // follows, so that their wait does not cover it)
+    auto enter = [&](int J) {
+      const int hh = J / nch;
+      if (hh != cur) {
+        close_head(cur);
+        cur = hh;
+        load_q(h0 + hh);
+        open_head(hh);
+        // every access of this path done (vmcnt(0), a wait the compiler's
+        // own wait insertion sees): otherwise its loads and stores count as
+        // pending on the path without a switch too, and the chunk loop waits
+        // for every chunk in flight before each fetch
+        __builtin_amdgcn_s_waitcnt(0x0f70);
+      }
+    };
+    // Chunk J is multiplied from LDS buffer J % 2 while chunk J + 1 is staged
+    // into the other (one barrier per chunk); register sets hold the chunks
+    // fetched ahead (DEPTH = 2: chunk c in kA/vA for even c, kB/vB for odd).
+    if (NJ > 0) {
+      stage(kA, vA, oA, 0);
+      fetchJ(min(DEPTH, NJ - 1), kA, vA, oA);  // chunk 2 (DEPTH = 1: chunk 1)
+    }
     if constexpr (DEPTH > 1) {
-      if (ncp < 2 && nch > 1) fetch(1, ncp, kB, vB, oB);
-      for (int j = 0; j < nch; j += 2) {
-        __syncthreads();  // every wave is done with the previous chunk
-        stage(kA, vA, oA);
+      for (int J = 0; J < NJ; J += 2) {
+        __syncthreads();  // buffer 0 holds chunk J; every wave is done with buffer 1
+        stage(kB, vB, oB, 1);  // chunk J + 1 (past the last: never read)
+        if (wave_busy) enter(J);
+        fetchJ(min(J + 3, NJ - 1), kB, vB, oB);
+        if (wave_busy) compute(J - cur * nch, nchp, 0);
+        if (J + 1 >= NJ) break;
         __syncthreads();
-        fetch(min(j + 2, nch - 1), ncp, kA, vA, oA);  // past the last: a re-read never staged
-        if (wave_busy) compute(j, ncp);
-        if (j + 1 >= nch) break;
-        __syncthreads();
-        stage(kB, vB, oB);
-        __syncthreads();
-        fetch(min(j + 3, nch - 1), ncp, kB, vB, oB);
-        if (wave_busy) compute(j + 1, ncp);
+        stage(kA, vA, oA, 0);  // chunk J + 2
+        if (wave_busy) enter(J + 1);
+        fetchJ(min(J + 4, NJ - 1), kA, vA, oA);
+        if (wave_busy) compute(J + 1 - cur * nch, nchp, 1);
       }
     } else {
-      for (int j = 0; j < nch; ++j) {
+      for (int J = 0; J < NJ; J += 2) {
         __syncthreads();
-        stage(kA, vA, oA);
+        stage(kA, vA, oA, 1);  // chunk J + 1
+        if (wave_busy) enter(J);
+        fetchJ(min(J + 2, NJ - 1), kA, vA, oA);
+        if (wave_busy) compute(J - cur * nch, nchp, 0);
+        if (J + 1 >= NJ) break;
         __syncthreads();
-        fetch(min(j + 1, nch - 1), ncp, kA, vA, oA);
-        if (wave_busy) compute(j, ncp);
+        stage(kA, vA, oA, 0);  // chunk J + 2
+        if (wave_busy) enter(J + 1);
+        fetchJ(min(J + 3, NJ - 1), kA, vA, oA);
+        if (wave_busy) compute(J + 1 - cur * nch, nchp, 1);
       }
     }
-  }
-  if (!q_ok) return;  // no barriers below
-  const float l_tot = xor32_sum(xor16_sum(l_run));
-  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  bf16_t* out = reinterpret_cast<bf16_t*>(a.out) + (int64_t)qi * d + head * HD + 4 * lg;
-#pragma unroll
-  for (int db = 0; db < 4; ++db) {
-    uint2 w;
-    w.x = pack_bf16x2(o[db][0] * inv, o[db][1] * inv);
-    w.y = pack_bf16x2(o[db][2] * inv, o[db][3] * inv);
-    *reinterpret_cast<uint2*>(out + 16 * db) = w;
+    if (wave_busy) {  // no chunks (nch = 0): the heads' own keys alone
+      close_head(cur);
+      for (int hh = cur + 1; hh < hg; ++hh) {
+        load_q(h0 + hh);
+        open_head(hh);
+        close_head(hh);
+      }
+    }
+  } else {
+    for (int eb = 0; eb < a.max_extra || eb == 0; eb += TREE_EB) {
+      const int ncols = build_columns(eb);
+      const int ncp = eb == 0 ? nchp : 0;  // prefix chunks go with the first batch
+      const int nch = ncp + (ncols + 63) / 64;
+      if (ncp < 1 && nch > 0) fetch(hbase(0), 0, ncp, kA, vA, oA);
+      if constexpr (DEPTH > 1) {
+        if (ncp < 2 && nch > 1) fetch(hbase(0), 1, ncp, kB, vB, oB);
+        for (int j = 0; j < nch; j += 2) {
+          __syncthreads();  // every wave is done with the previous chunk
+          stage(kA, vA, oA);
+          __syncthreads();
+          fetch(hbase(0), min(j + 2, nch - 1), ncp, kA, vA, oA);  // past the last: a re-read never staged
+          if (wave_busy) compute(j, ncp);
+          if (j + 1 >= nch) break;
+          __syncthreads();
+          stage(kB, vB, oB);
+          __syncthreads();
+          fetch(hbase(0), min(j + 3, nch - 1), ncp, kB, vB, oB);
+          if (wave_busy) compute(j + 1, ncp);
+        }
+      } else {
+        for (int j = 0; j < nch; ++j) {
+          __syncthreads();
+          stage(kA, vA, oA);
+          __syncthreads();
+          fetch(hbase(0), min(j + 1, nch - 1), ncp, kA, vA, oA);
+          if (wave_busy) compute(j, ncp);
+        }
+      }
+    }
+    close_head(0);  // no barriers there
   }
 }
 
@@ -1203,16 +1328,42 @@ hipError_t launch_attn_extend_fan(const ExtendAttnArgs& a, int g0, int g1, int w
   return hipGetLastError();
 }
 
-hipError_t launch_attn_extend_tree(const ExtendAttnArgs& a, hipStream_t st) {
-  if (!a.self_slot || a.max_blocks > TREE_MAX_BLOCKS) return hipErrorInvalidValue;
-  if (!a.act_bf16 || a.tiles == nullptr) return hipErrorInvalidValue;
-  if (a.n_tiles == 0) return hipSuccess;
-  if (a.tile_q == 128)  // 8 waves, two chunks in flight
-    launch_timed(attn_extend_tree_kernel<8, 2>, dim3(a.n_tiles, a.n_head), dim3(512), 0, st, a);
-  else if (a.tile_q == 64)  // 4 waves, one chunk in flight (registers)
-    launch_timed(attn_extend_tree_kernel<4, 1>, dim3(a.n_tiles, a.n_head), dim3(256), 0, st, a);
-  else
+#ifndef ALLIE_TREE_MIN_WG
+#define ALLIE_TREE_MIN_WG 1024
+#endif
+// Heads per tree workgroup (one column batch only, else 1): the caller's
+// a.head_group when it divides the head count; for 0 the largest of 16, 8,
+// 4, 2 that divides it and still leaves at least ALLIE_TREE_MIN_WG
+// workgroups (two rounds of two per CU); else 1.
+int tree_head_group(const ExtendAttnArgs& a) {
+  if (a.max_extra > TREE_EB) return 1;
+  if (a.head_group > 0) return a.n_head % a.head_group == 0 ? a.head_group : 1;
+  for (int hg = 16; hg > 1; hg >>= 1)
+    if (a.n_head % hg == 0 && (int64_t)a.n_tiles * (a.n_head / hg) >= ALLIE_TREE_MIN_WG) return hg;
+  return 1;
+}
+
+hipError_t launch_attn_extend_tree(const ExtendAttnArgs& a0, hipStream_t st) {
+  if (!a0.self_slot || a0.max_blocks > TREE_MAX_BLOCKS) return hipErrorInvalidValue;
+  if (!a0.act_bf16 || a0.tiles == nullptr) return hipErrorInvalidValue;
+  if (a0.n_tiles == 0) return hipSuccess;
+  ExtendAttnArgs a = a0;
+  a.head_group = tree_head_group(a0);
+  const dim3 grid(a.n_tiles, a.n_head / a.head_group);
+  const bool mh = a.head_group > 1;
+  if (a.tile_q == 128) {  // 8 waves, two chunks in flight
+    if (mh)
+      launch_timed(attn_extend_tree_kernel<8, 2, true>, grid, dim3(512), 0, st, a);
+    else
+      launch_timed(attn_extend_tree_kernel<8, 2, false>, grid, dim3(512), 0, st, a);
+  } else if (a.tile_q == 64) {  // 4 waves, one chunk in flight (registers)
+    if (mh)
+      launch_timed(attn_extend_tree_kernel<4, 1, true>, grid, dim3(256), 0, st, a);
+    else
+      launch_timed(attn_extend_tree_kernel<4, 1, false>, grid, dim3(256), 0, st, a);
+  } else {
     return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -146,6 +146,7 @@ struct allie_model {
   hipStream_t side[2] = {nullptr, nullptr};
   hipEvent_t fork = nullptr, join[2] = {nullptr, nullptr};
   // two-stream split thresholds (allie_model_set_split_tokens; 0: never)
+  int tree_heads = 0;  // heads per tree-attention workgroup (allie_model_set_tree_heads; 0: automatic)
   int64_t split_tokens = 24576;  // a prefill's tokens, an extend's tokens
   int64_t split_decode = 512;    // an extend's one-token groups (decode steps)
 };
@@ -981,6 +982,14 @@ int allie_model_set_split_tokens(allie_model* m, int64_t tokens, int64_t decode_
   return ALLIE_OK;
 }
 
+int allie_model_set_tree_heads(allie_model* m, int heads) {
+  if (!m) return fail(ALLIE_ERR_ARG, "null model");
+  if (heads < 0 || heads > 16 || (heads > 0 && m->H % heads != 0))
+    return fail(ALLIE_ERR_ARG, "tree heads %d: 0, or a divisor of %d heads up to 16", heads, m->H);
+  m->tree_heads = heads;
+  return ALLIE_OK;
+}
+
 int allie_model_finalize(allie_model* m) {
   if (!m) return fail(ALLIE_ERR_ARG, "model is NULL");
   for (int k = ALLIE_W_WTE; k <= ALLIE_W_TIME_B; ++k)
@@ -1280,6 +1289,7 @@ int extend_run(allie_model* m, const ExtendPlan& plan, const ExtendWS& w, const 
   xa.out = w.attn;
   xa.act_bf16 = act;
   xa.self_slot = w.self_slot;  // written by the prepare step above
+  xa.head_group = m->tree_heads;
 
   // one-token groups (decode steps) [0, n_dec) stream their keys with one
   // wave per (token, head), the games with the most keys first (bf16)

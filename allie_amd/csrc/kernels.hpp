@@ -225,6 +225,7 @@ struct ExtendAttnArgs {
   int act_bf16;
   const int32_t* order;        // wave kernel: token of the i-th (token, head) row, or null (identity)
   const int32_t* self_slot;    // tree kernel: [n] each token's own pool slot (its last extra; -1: none)
+  int head_group;              // tree kernel: heads per workgroup (set by its launcher)
 };
 // one wave per (token, head), any group sizes, bf16 or fp32
 hipError_t launch_attn_extend_wave(const ExtendAttnArgs& a, hipStream_t st);

@@ -297,6 +297,11 @@ class Engine:
         capi.check(self._lib.allie_model_set_split_tokens(self._m, int(tokens), int(decode_tokens)),
                    "allie_model_set_split_tokens")
 
+    def set_tree_heads(self, heads: int) -> None:
+        """Heads per tree-attention workgroup (``allie_model_set_tree_heads``):
+        0 chooses by the launch size; the results are the same bits either way."""
+        capi.check(self._lib.allie_model_set_tree_heads(self._m, int(heads)), "allie_model_set_tree_heads")
+
     def close(self) -> None:
         if getattr(self, "_m", None):
             self._lib.allie_model_destroy(self._m)

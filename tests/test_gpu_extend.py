@@ -196,6 +196,66 @@ def test_tree_levels_match_full_recompute(tiny, mode, tol, prefix, kids, cuda):
     eng.close()
 
 
+# level-1 children per root: level 2 then holds groups of 300 and 18 tokens
+# (128-query tiles) or of 40 and 60 (64-query tiles)
+@pytest.mark.parametrize("kids", [[150, 9], [20, 30]])
+def test_tree_head_groups_same_bits(tiny, kids, cuda):
+    """The tree kernel taking 1, 2 or 4 heads per workgroup gives the same
+    bits at every level; level 2 also against the oracle.  A group of fresh
+    one-token games (no prefix, no other private key) covers heads with no
+    key chunks at all."""
+    cfg, sd = tiny
+    assert cfg.n_head == 4
+    rng = np.random.default_rng(21)
+    prefix = [37, 100]
+    R = len(prefix)
+    roots = [list(rng.integers(0, 1968, n)) for n in prefix]
+    n1 = sum(kids)
+    ids1 = rng.integers(0, 1968, n1)
+    root_of1 = np.repeat(np.arange(R), kids)
+    pos1 = np.array([prefix[r] for r in root_of1], np.int32)
+    par = np.repeat(np.arange(n1), 2)
+    n2 = len(par)
+    ids2 = rng.integers(0, 1968, n2)
+    pos2 = pos1[par] + 1
+    sizes2 = [2 * k for k in kids]
+    n3 = 20
+    ids3 = rng.integers(0, 1968, n3)
+    results = {}
+    for hg in (1, 2, 4):
+        eng = Engine(cfg, sd, mode="bfloat16")
+        eng.set_tree_heads(hg)
+        node_base = R * BPG
+        pool = nan_pool(eng, node_base + (n1 + n2 + n3 + 15) // 16 + 1)
+        table = torch.tensor([[r * BPG + j for j in range(BPG)] for r in range(R)], dtype=torch.int32, device=cuda)
+        eng.prefill(np.concatenate([np.asarray(x, np.uint32) for x in roots]), np.array(prefix, np.int32),
+                    kv_pool=pool, kv_block_table=table)
+        status = torch.zeros(1, dtype=torch.int32, device=cuda)
+        slot1 = node_base * 16 + np.arange(n1, dtype=np.int32)
+        out1 = eng.extend(ids1, pos1, kids, prefix, table, slot1[:, None], np.ones(n1, np.int32), pool, status=status)
+        slot2 = node_base * 16 + n1 + np.arange(n2, dtype=np.int32)
+        extra = np.stack([slot1[par], slot2], axis=1).astype(np.int32)
+        out2 = eng.extend(ids2, pos2, sizes2, prefix, table, extra, np.full(n2, 2, np.int32), pool, status=status)
+        slot3 = node_base * 16 + n1 + n2 + np.arange(n3, dtype=np.int32)
+        out3 = eng.extend(ids3, np.zeros(n3, np.int32), [n3], [0], table[:1], slot3[:, None], np.ones(n3, np.int32),
+                          pool, status=status)
+        torch.cuda.synchronize()
+        assert int(status.item()) == 0
+        results[hg] = [{k: getattr(o, k).cpu().numpy().copy() for k in ("logits", "value", "time", "top1")}
+                       for o in (out1, out2, out3)]
+        if hg == 1:
+            oracle = RefModel(cfg, sd, mode="bfloat16")
+            paths1 = [roots[root_of1[i]] + [int(ids1[i])] for i in range(n1)]
+            paths2 = [paths1[par[i]] + [int(ids2[i])] for i in range(n2)]
+            check(out2, oracle.forward_last([np.asarray(p, np.int64) for p in paths2]), 2e-2, "level 2")
+            check(out3, oracle.forward_last([np.asarray([t], np.int64) for t in ids3]), 2e-2, "fresh games")
+        eng.close()
+    for hg in (2, 4):
+        for lvl, (a, b) in enumerate(zip(results[1], results[hg])):
+            for k in a:
+                assert np.array_equal(a[k], b[k]), (hg, lvl, k)
+
+
 # (tokens of the two new games over extras, tokens of the new game over its own
 # prefix): with 70 the batch takes the tree kernel, with groups of at most 16
 # the split-prefix kernels (a group with an empty prefix among them)
