@@ -105,3 +105,60 @@ def test_noalloc_2x_fp8_max_tokens(cuda):
     b2 = batch(rng, table, 200, [1, 3], 1, 2, slot0 + 300)
     run_both(eng, pool, b2)
     eng.close()
+
+
+def test_noalloc_captured_with_allocation_forbidden(cuda):
+    """The allocation-free extend captured into a HIP graph in the strictest
+    capture mode (``global``: an allocation or free call from any thread
+    during the capture fails it), then replayed three times with the
+    allocating ``allie_extend`` run eagerly in between, each replay equal to
+    it bit for bit; torch's allocator reserves nothing more across an eager
+    call either."""
+    from allie_amd.engine import PrefillResult
+
+    cfg = config.TINY
+    eng = Engine(cfg, weights.init_weights(cfg, seed=5, perturb=True), mode="bfloat16")
+    pool, table, free = roots(eng, 4, 37, seed=1)
+    rng = np.random.default_rng(8)
+    b = batch(rng, table, 37, [0, 1, 2, 3, 2], 5, 2, free * 16)  # 25 tokens, fan kernel
+    dev = eng.device
+    n, G = len(b["ids"]), len(b["group_sizes"])
+    gs = np.zeros(G + 1, np.int32)
+    gs[1:] = np.cumsum(b["group_sizes"])
+    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(dev)
+    ids, pos, gsd, pl = i32(b["ids"]), i32(b["pos"]), i32(gs), i32(b["prefix_len"])
+    pb = b["prefix_blocks"].to(dtype=torch.int32).contiguous()
+    ex, ne = i32(b["extra_slot"]), i32(b["n_extra"])
+    V = cfg.vocab_size
+    out = PrefillResult(logits=torch.zeros(n, V, device=dev), value=torch.zeros(n, device=dev),
+                        time=torch.zeros(n, device=dev), top1=torch.zeros(n, dtype=torch.int32, device=dev),
+                        max_logit=torch.zeros(n, device=dev), lse=torch.zeros(n, device=dev))
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def launch():
+        eng.extend_noalloc_raw(ids, pos, gs, gsd, pl, pb, ex, ne, pool, out, status)
+
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launch()  # warm-up
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    before = (torch.cuda.memory_allocated(dev), torch.cuda.memory_reserved(dev))
+    launch()
+    torch.cuda.synchronize()
+    assert (torch.cuda.memory_allocated(dev), torch.cuda.memory_reserved(dev)) == before
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, capture_error_mode="global"):
+        launch()
+    for rep in range(3):
+        for f in FIELDS:
+            getattr(out, f).zero_()
+        status.fill_(-1)
+        g.replay()
+        ref = eng.extend(**b, kv_pool=pool)  # eager, allocating, between the replays
+        torch.cuda.synchronize()
+        assert int(status.item()) == 0, rep
+        for f in FIELDS:
+            assert torch.equal(getattr(out, f), getattr(ref, f)), (rep, f)
+    eng.close()
