@@ -1328,18 +1328,19 @@ hipError_t launch_attn_extend_fan(const ExtendAttnArgs& a, int g0, int g1, int w
   return hipGetLastError();
 }
 
-#ifndef ALLIE_TREE_MIN_WG
-#define ALLIE_TREE_MIN_WG 1024
-#endif
+constexpr int TREE_MIN_WG = 1024;  // two rounds of two 8-wave workgroups per CU
 // Heads per tree workgroup (one column batch only, else 1): the caller's
-// a.head_group when it divides the head count; for 0 the largest of 16, 8,
-// 4, 2 that divides it and still leaves at least ALLIE_TREE_MIN_WG
-// workgroups (two rounds of two per CU); else 1.
+// a.head_group when it divides the head count; for 0, on 128-query tiles,
+// the largest of 16, 8, 4, 2 that divides it and still leaves at least
+// TREE_MIN_WG workgroups; else 1.  (The 64-query, one-chunk-in-registers
+// instance with several heads spills registers, so 0 keeps those tiles at
+// one head; it runs only when a caller asks for it.)
 int tree_head_group(const ExtendAttnArgs& a) {
   if (a.max_extra > TREE_EB) return 1;
   if (a.head_group > 0) return a.n_head % a.head_group == 0 ? a.head_group : 1;
+  if (a.tile_q != 128) return 1;
   for (int hg = 16; hg > 1; hg >>= 1)
-    if (a.n_head % hg == 0 && (int64_t)a.n_tiles * (a.n_head / hg) >= ALLIE_TREE_MIN_WG) return hg;
+    if (a.n_head % hg == 0 && (int64_t)a.n_tiles * (a.n_head / hg) >= TREE_MIN_WG) return hg;
   return 1;
 }
 

@@ -112,8 +112,9 @@ int allie_model_finalize(allie_model* m);
 int allie_model_set_split_tokens(allie_model* m, int64_t tokens, int64_t decode_tokens);
 /* Heads per workgroup of the tree attention kernel (bf16 extends whose groups
  * exceed 16 tokens, with at most 8 private keys per token): 0 (the default)
- * picks the largest of 16, 8, 4, 2 dividing the head count that still leaves
- * at least 1,024 workgroups; a divisor of the head count up to 16 forces it.
+ * picks, for 128-query tiles (some group over 64 tokens), the largest of 16,
+ * 8, 4, 2 dividing the head count that still leaves at least 1,024
+ * workgroups, else one head; a divisor of the head count up to 16 forces it.
  * Every head's arithmetic is the same whatever the grouping, so the results
  * are the same bits.  No reference counterpart: a tuning knob. */
 int allie_model_set_tree_heads(allie_model* m, int heads);
