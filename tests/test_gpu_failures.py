@@ -99,6 +99,20 @@ def test_prefill_kv_pool_too_small(tiny, cuda):
     eng.close()
 
 
+def test_tree_heads_knob_rejects_non_divisors(tiny, cuda):
+    """allie_model_set_tree_heads takes 0 or a divisor of the head count up
+    to 16 (the tiny model has 4 heads); anything else fails before any launch
+    and leaves the setting as it was."""
+    cfg, sd = tiny
+    eng = Engine(cfg, sd, mode="bfloat16")
+    for bad in (3, -1, 32):
+        with pytest.raises(capi.AllieError, match="tree heads"):
+            eng.set_tree_heads(bad)
+    for ok in (0, 1, 2, 4):
+        eng.set_tree_heads(ok)
+    eng.close()
+
+
 def test_packer_status_reaches_the_caller(tiny, cuda):
     cfg, sd = tiny
     seqs, lens = games(5, 4, 10, 30)
