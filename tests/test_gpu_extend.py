@@ -256,6 +256,50 @@ def test_tree_head_groups_same_bits(tiny, kids, cuda):
                 assert np.array_equal(a[k], b[k]), (hg, lvl, k)
 
 
+@pytest.mark.parametrize("depth", [8, 9])
+def test_tree_head_groups_deep_private_keys(tiny, depth, cuda):
+    """Tokens with `depth` private keys (ancestor slots shared by runs of 10
+    siblings, then the token's own): with 8 the column build is one batch and
+    1, 2 or 4 heads per workgroup give the same bits; with 9 it takes two
+    batches and every setting runs one head per workgroup (same bits too).
+    The ancestors' slots are read as written by nothing but the zeroed pool."""
+    cfg, sd = tiny
+    rng = np.random.default_rng(31)
+    prefix = [50, 90]
+    sizes = [70, 30]
+    n = sum(sizes)
+    roots = [rng.integers(0, 1968, p) for p in prefix]
+    ids = rng.integers(0, 1968, n)
+    node_base = len(prefix) * BPG
+    anc = node_base * 16 + np.arange(n * depth, dtype=np.int32)  # fresh ancestor slots
+    extra = np.zeros((n, depth), np.int32)
+    for i in range(n):
+        for e in range(depth - 1):
+            extra[i, e] = anc[(i // 10) * depth + e]  # shared by runs of 10 tokens
+        extra[i, depth - 1] = anc[-1 - i]  # own slot
+    root_of = np.repeat(np.arange(len(prefix)), sizes)
+    pos = np.array([prefix[r] + depth - 1 for r in root_of], np.int32)
+    outs = {}
+    for hg in (1, 2, 4):
+        eng = Engine(cfg, sd, mode="bfloat16")
+        eng.set_tree_heads(hg)
+        pool = eng.new_kv_pool(node_base + (len(anc) + 15) // 16 + 1).zero_()
+        table = torch.tensor([[r * BPG + j for j in range(BPG)] for r in range(len(prefix))],
+                             dtype=torch.int32, device=cuda)
+        eng.prefill(np.concatenate([np.asarray(x, np.uint32) for x in roots]), np.array(prefix, np.int32),
+                    kv_pool=pool, kv_block_table=table)
+        status = torch.zeros(1, dtype=torch.int32, device=cuda)
+        out = eng.extend(ids, pos, sizes, prefix, table, extra, np.full(n, depth, np.int32), pool, status=status)
+        torch.cuda.synchronize()
+        assert int(status.item()) == 0
+        assert torch.isfinite(out.logits).all()
+        outs[hg] = {k: getattr(out, k).cpu().numpy().copy() for k in ("logits", "value", "time", "top1")}
+        eng.close()
+    for hg in (2, 4):
+        for k in outs[1]:
+            assert np.array_equal(outs[1][k], outs[hg][k]), (depth, hg, k)
+
+
 # (tokens of the two new games over extras, tokens of the new game over its own
 # prefix): with 70 the batch takes the tree kernel, with groups of at most 16
 # the split-prefix kernels (a group with an empty prefix among them)
