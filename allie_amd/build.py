@@ -21,8 +21,9 @@ LIB = os.path.join(HERE, "liballie_amd.so")
 CHESS_LIB = os.path.join(HERE, "liballie_chess.so")
 ARCH = os.environ.get("ALLIE_OFFLOAD_ARCH", "gfx950")
 
-# Packed fp32 instructions are kept out of every kernel (see DESIGN notes on
-# this pool); the host pass warns that it does not know the feature.
+# Packed fp32 instructions (v_pk_*_f32) are kept out of every kernel: some of
+# their forms have given wrong results now and then on the MI355X boxes this
+# was built on; the host pass warns that it does not know the feature.
 FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",

@@ -717,7 +717,7 @@ def bench_search(args):
                       note="kv replays each leaf from a captured HIP graph, kv_eager launches it kernel by "
                            "kernel; kv_batch16 is a different (virtual-loss batched) search; recompute, kv and "
                            "kv_eager make the same decisions")
-    res["metric"] = "MCTS simulations/s per decision (not a SURVEY headline metric)"
+    res["metric"] = "MCTS simulations/s per decision (not the headline metric)"
     res["roofline"] = None
     res["cpu_baseline"] = None
     return res
@@ -780,7 +780,7 @@ def bench_serve(args):
                       "games of 20-120 plies",
                       sequential_requests_per_s=seq_rps, speedup_vs_sequential=rps / seq_rps,
                       mean_batch=reqs / max(batches, 1))
-    res["metric"] = "policy requests/s (not a SURVEY headline metric)"
+    res["metric"] = "policy requests/s (not the headline metric)"
     res["roofline"] = None
     res["cpu_baseline"] = None
     return res
@@ -802,7 +802,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                                   "(the path shards by game with no exchange; see DESIGN.md)"}))
+                                   "(games never exchange data, so the batch would shard by game, one "
+                                   "shard per GPU)"}))
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy()
