@@ -817,7 +817,7 @@ int allie_model_create(const allie_config* cfg, allie_model** out) {
   // zero padding rows of the heads matrix and unset biases
   e = hipMemset(m->arena, 0, m->arena_bytes);
   if (e != hipSuccess) {
-    hipFree(m->arena);
+    (void)hipFree(m->arena);
     delete m;
     return fail(ALLIE_ERR_HIP, "hipMemset: %s", hipGetErrorString(e));
   }
@@ -840,22 +840,24 @@ int allie_model_create(const allie_config* cfg, allie_model** out) {
 
 void allie_model_destroy(allie_model* m) {
   if (!m) return;
+  // teardown: a failing release has no caller to report to, so results are
+  // not checked here
   for (int i = 0; i < 2; ++i) {
     if (m->side[i]) {
-      hipStreamSynchronize(m->side[i]);
-      hipStreamDestroy(m->side[i]);
+      (void)hipStreamSynchronize(m->side[i]);
+      (void)hipStreamDestroy(m->side[i]);
     }
-    if (m->join[i]) hipEventDestroy(m->join[i]);
+    if (m->join[i]) (void)hipEventDestroy(m->join[i]);
   }
-  if (m->fork) hipEventDestroy(m->fork);
+  if (m->fork) (void)hipEventDestroy(m->fork);
   for (int i = 0; i < PinnedRing::N; ++i) {
     if (m->pinned.ev[i]) {
-      hipEventSynchronize(m->pinned.ev[i]);
-      hipEventDestroy(m->pinned.ev[i]);
+      (void)hipEventSynchronize(m->pinned.ev[i]);
+      (void)hipEventDestroy(m->pinned.ev[i]);
     }
-    if (m->pinned.buf[i]) hipHostFree(m->pinned.buf[i]);
+    if (m->pinned.buf[i]) (void)hipHostFree(m->pinned.buf[i]);
   }
-  if (m->arena) hipFree(m->arena);
+  if (m->arena) (void)hipFree(m->arena);
   delete m;
 }
 
@@ -1446,8 +1448,8 @@ int allie_extend_noalloc(allie_model* m, const int32_t* ids, const int32_t* pos,
 int allie_probe_begin(int kind, int max_launches) {
   if (kind < ALLIE_PROBE_QKV || kind > ALLIE_PROBE_DECODE || max_launches <= 0)
     return fail(ALLIE_ERR_ARG, "bad probe arguments");
-  for (auto e : g_probe.start) hipEventDestroy(e);
-  for (auto e : g_probe.stop) hipEventDestroy(e);
+  for (auto e : g_probe.start) (void)hipEventDestroy(e);
+  for (auto e : g_probe.stop) (void)hipEventDestroy(e);
   g_probe = Probe();
   g_probe.start.resize(max_launches);
   g_probe.stop.resize(max_launches);
@@ -1494,8 +1496,8 @@ int allie_probe_end(float* total_ms_host, int* n_launches_host) {
     HIP_TRY(hipEventElapsedTime(&ms, g_probe.start[i], g_probe.stop[i]));
     tot += ms;
   }
-  for (auto e : g_probe.start) hipEventDestroy(e);
-  for (auto e : g_probe.stop) hipEventDestroy(e);
+  for (auto e : g_probe.start) (void)hipEventDestroy(e);
+  for (auto e : g_probe.stop) (void)hipEventDestroy(e);
   g_probe = Probe();
   *total_ms_host = tot;
   *n_launches_host = n;
